@@ -1,0 +1,210 @@
+#!/usr/bin/env python3
+"""Benchmark of the paia_gemv hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH]
+
+Workload (the metric's configuration): FP8 W8A16 M=1 GEMVs at the Llama-3.1-8B per-layer shapes
+qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336, OCP e4m3fn weights with a per-row fp32 scale, bf16
+activations and outputs. One step = the four GEMVs of one decoder layer; steps rotate over L distinct layer copies
+whose total (>= 4 x 256 MiB) defeats the Infinity Cache, so every weight byte comes from HBM. The timed region is one
+hipGraph replay of K steps, bracketed by device synchronisation, with all inputs resident in HBM.
+
+Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmic GB/s of the step, plus
+  per_gemv      us/GEMV, GB/s and % of 8 TB/s for each shape (graph of R back-to-back launches, rotating copies)
+  roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time, vs 8 TB/s
+  cpu_baseline  the reference's CPU path (dequantise, then fp32 matmul) on the host cores, on a bounded sample
+Copy 0 of every operand set is checked against the CPU oracle before anything is timed.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "paia-project_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "µs/GEMV + achieved HBM GB/s (% of 8 TB/s), Llama-3.1-8B shapes, batch 1"
+PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
+    """The reference's CPU path: dequantise with the oracle (C, one thread), then an fp32 torch
+    matmul on the host cores. Runs over the layer's four shapes (seeded copy-0 operands) until ~budget_s."""
+    import numpy as np
+    import torch
+    from paia_bench.inputs import as_numpy
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64"))))
+    torch.set_num_threads(threads)
+    t_deq = t_mm = 0.0
+    nbytes = 0
+    steps = 0
+    t_start = time.perf_counter()
+    while True:
+        for c in cases:
+            a = as_numpy(c.ops0)
+            t0 = time.perf_counter()
+            Wd = oracle.dequant_fp8(a["Wq"], a["scale"])
+            t1 = time.perf_counter()
+            x = torch.from_numpy(oracle.bf16_bits_to_f32(a["x"]).copy())
+            y = torch.from_numpy(Wd) @ x
+            y = y.to(torch.bfloat16)
+            t2 = time.perf_counter()
+            t_deq += t1 - t0
+            t_mm += t2 - t1
+            nbytes += c.bytes()["total"]
+            del Wd, y
+        steps += 1
+        if time.perf_counter() - t_start > budget_s or steps >= 20:
+            break
+    total = t_deq + t_mm
+    import platform
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        model = platform.processor()
+    return {"value": nbytes / total / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} layer step(s) x 4 FP8 GEMVs (Llama-3.1-8B qkv/o/gate_up/down, seeded copy 0): "
+                      f"oracle dequant (1 thread) + torch fp32 matmul ({threads} threads); "
+                      f"us per layer step {total / steps * 1e6:.0f} (dequant {t_deq / steps * 1e6:.0f}, "
+                      f"matmul {t_mm / steps * 1e6:.0f}); cpu {model}",
+            "matmul_only_gbps": nbytes / t_mm / 1e9 if t_mm > 0 else None}
+
+
+def load_traffic(kernel_key: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (profiles/), or None."""
+    f = ROOT / "profiles" / "pmc_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get(kernel_key, {}).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--report", type=str, default=None, help="also write a detailed JSON report here")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    a = ap.parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the M=1 GEMV shards along N "
+              "with no collective, so N-GPU throughput is N x the one-GPU figure on N/N-row shards. Run --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from oracle import oracle
+    from paia_bench.cases import GemvCase
+    from paia_bench.timing import LLC_BYTES, capture, time_per_call_us
+    from paia_gemv import load_lib
+    from paia_gemv.shapes import LAYER
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        return 3
+    lib = load_lib()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} CUs {props.multi_processor_count} lib {lib.path}")
+
+    shapes = LAYER["llama31_8b"]
+    cases = [GemvCase(lib, "fp8", N, K, name=f"fp8_{nm}_{N}x{K}") for nm, N, K in shapes]
+    layer_bytes = sum(c.footprint() for c in cases)
+    L = max(2, math.ceil(4 * LLC_BYTES / layer_bytes))
+    for c in cases:
+        c.build(L, dev)
+    log(f"built {L} layer copies ({L * layer_bytes / 2**30:.2f} GiB); checking copy 0 against the oracle")
+    for c in cases:
+        chk = c.check(oracle)
+        log(f"  {c.name}: variant {c.variant} rel_err {chk['rel_err']:.2e} ok {chk['ok']}")
+        if not chk["ok"]:
+            print(json.dumps({"error": f"{c.name} failed the correctness gate", **chk}))
+            return 1
+
+    step_bytes = sum(c.bytes()["total"] for c in cases)
+
+    def steps_fn(n):
+        def run():
+            for s in range(n):
+                for c in cases:
+                    c.call(s % L)
+        return run
+
+    g_warm = capture(steps_fn(max(1, a.warmup)), warm=1)
+    g_timed = capture(steps_fn(a.steps), warm=0)
+    g_warm.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    g_timed.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / a.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"timed {a.steps} steps: {gpu_ms:.3f} ms (wall {wall_ms:.3f} ms), {ms_per_step * 1e3:.2f} us/step, "
+        f"{value:.0f} GB/s")
+    del g_warm, g_timed
+
+    per = {}
+    for c in cases:
+        t = time_per_call_us(c.call, L)
+        gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
+        per[c.name] = {"us": round(t["us"], 3), "gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1),
+                       "variant": lib.variants_fp8[c.variant], "bytes": c.bytes()["total"], "R": t["R"]}
+        log(f"  {c.name}: {t['us']:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s)")
+
+    dom = max(cases, key=lambda c: c.bytes()["total"])
+    dom_us = per[dom.name]["us"]
+    achieved = dom.bytes()["total"] / (dom_us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBPS, 4), "traffic": load_traffic(dom.name),
+            "kernel": dom.name, "avg_launch_us": dom_us, "algorithmic_bytes": dom.bytes()["total"]}
+
+    cpu = None
+    if not a.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(oracle, cases)
+        log(f"  cpu {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+
+    out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+           "warmup": a.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp8_e4m3 weights x bf16 activations, fp32 accumulate",
+           "data": "synthetic (seeded N(0,0.02) weights quantised to e4m3fn; N(0,1) bf16 x)",
+           "config": {"workload": "FP8 W8A16 GEMV, M=1, Llama-3.1-8B layer: qkv 6144x4096, o 4096x4096, "
+                                  "gate_up 28672x4096, down 4096x14336 (BASELINE configs[1])",
+                      "layer_copies": L, "rotation_bytes": L * layer_bytes, "step_bytes": step_bytes,
+                      "us_per_layer_step": round(ms_per_step * 1e3, 3),
+                      "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1)},
+           "per_gemv": per, "roofline": roof, "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+    if a.report:
+        Path(a.report).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.report).write_text(json.dumps(out, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

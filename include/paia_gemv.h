@@ -1,0 +1,94 @@
+/* paia_gemv.h -- C ABI of libpaia_gemv.so, the gfx950 (MI355X) HIP build of the PAIA M=1 GEMV family.
+ *
+ * Drop-in for the reference's ctypes-loaded libpaia_gemv.so (Bejaine/PAIA-Project, src/paia_gemv/): the first eleven
+ * entry points keep the reference's names, argument order, argument meaning, alignment contract and return codes.
+ * The rest are additions for the BASELINE configurations (bias epilogue, asymmetric INT4, on-device dequantisation).
+ *
+ * Conventions (all entry points, as src/paia_gemv/gemv_quant.cu:2 and gemv_bf16.cu:44-47):
+ *   return 0 ok; -1 bad variant index; -2 bad shape or alignment; > 0 a hipError_t reported after the launch.
+ *   All pointers are caller-owned device memory. The library allocates nothing, keeps no handles, never
+ *   synchronises, and launches on `stream` (a hipStream_t; NULL = the null stream), so calls are graph-capturable.
+ *   x, y and bias are bf16 bit patterns; N, K are ints with size_t offsets inside.
+ *   y[n] = bf16_round_to_nearest_even( sum_k deq(W[n,k]) * x[k] (+ bias[n]) ), fp32 accumulation.
+ *
+ * gfx950 limit that the reference does not have: x is staged in LDS, so K is bounded by 64 KiB of LDS per block:
+ *   BF16 and FP8 K <= 32768, INT4 K <= 30720 (all Llama-3.1-8B / Qwen2.5-7B shapes fit); larger K returns -2.
+ */
+#ifndef PAIA_GEMV_H
+#define PAIA_GEMV_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PAIA_API __attribute__((visibility("default")))
+
+/* ---- BF16: W bf16 [N][K] row-major. K % 8 == 0; W, x, y 16-byte aligned. ---------------------------------- */
+
+/* replaces src/paia_gemv/gemv_bf16.cu:38 */
+PAIA_API int paia_gemv_bf16_variant_count(void);
+/* replaces src/paia_gemv/gemv_bf16.cu:41-45. Knobs (gfx950 meaning): R rows per wave, U 16-byte loads per row per
+ * batch, W waves per block, S nontemporal weight loads, H split-K across the waves of a block. */
+PAIA_API int paia_gemv_bf16_variant_info(int v, int* R, int* U, int* W, int* S, int* H);
+/* replaces src/paia_gemv/gemv_bf16.cu:48-53 */
+PAIA_API int paia_gemv_bf16(const void* W, const void* x, void* y, int N, int K, int variant, void* stream);
+/* no reference counterpart (BASELINE Qwen qkv bias epilogue): bias bf16 [N], 2-byte aligned, or NULL */
+PAIA_API int paia_gemv_bf16_bias(const void* W, const void* x, const void* bias, void* y, int N, int K, int variant,
+                                 void* stream);
+
+/* ---- FP8 W8A16: Wq e4m3fn [N][K], scale fp32 [N]. K % 16 == 0; Wq, x 16-byte, scale 4-byte, y 2-byte aligned. -- */
+
+/* replaces src/paia_gemv/gemv_quant.cu:61 */
+PAIA_API int paia_gemv_fp8_variant_count(void);
+/* replaces src/paia_gemv/gemv_quant.cu:62 */
+PAIA_API int paia_gemv_fp8_variant_info(int v, int* R, int* U, int* W, int* H);
+/* replaces src/paia_gemv/gemv_quant.cu:64-68 */
+PAIA_API int paia_gemv_fp8(const void* Wq, const void* scale, const void* x, void* y, int N, int K, int variant,
+                           void* stream);
+/* no reference counterpart (bias epilogue for the FP8 Qwen qkv config): bias bf16 [N] or NULL */
+PAIA_API int paia_gemv_fp8_bias(const void* Wq, const void* scale, const void* x, const void* bias, void* y, int N,
+                                int K, int variant, void* stream);
+
+/* ---- INT4 W4A16 g128, reference format: Wq [N][K/2] (byte j = weights 2j low nibble, 2j+1 high nibble, i.e. 8 per
+ *      int32 along K), zero point 8, scales fp16 [N][K/128]. K % 128 == 0; Wq, x 16-byte, scales, y 2-byte. ----- */
+
+/* replaces src/paia_gemv/gemv_quant.cu:70 */
+PAIA_API int paia_gemv_int4_variant_count(void);
+/* replaces src/paia_gemv/gemv_quant.cu:71 */
+PAIA_API int paia_gemv_int4_variant_info(int v, int* R, int* U, int* W, int* H);
+/* replaces src/paia_gemv/gemv_quant.cu:73-77 */
+PAIA_API int paia_gemv_int4(const void* Wq, const void* scales, const void* x, void* y, int N, int K, int variant,
+                            void* stream);
+/* replaces src/paia_gemv/gemv_quant.cu:80-85 (the naive K1 control) */
+PAIA_API int paia_gemv_int4_naive(const void* Wq, const void* scales, const void* x, void* y, int N, int K,
+                                  void* stream);
+/* replaces src/paia_gemv/gemv_quant.cu:88-97 (the unfused control): scratch_bf16 is caller-owned, 2*N*K bytes,
+ * 16-byte aligned; y must satisfy the BF16 contract (16-byte aligned). */
+PAIA_API int paia_gemv_int4_unfused(const void* Wq, const void* scales, const void* x, void* y, void* scratch_bf16,
+                                    int N, int K, void* stream);
+
+/* ---- INT4 W4A16 g128, asymmetric format (no reference counterpart; BASELINE INT4 configs): q in 0..15 packed as
+ *      above, scales bf16 [N][G] (G = K/128), zeros [N][ceil(G/2)] bytes (group 2j low nibble, 2j+1 high nibble),
+ *      dequant (q - z) * s; optional bias bf16 [N] (or NULL). Uses the paia_gemv_int4 variant table. --------- */
+PAIA_API int paia_gemv_int4_zp(const void* Wq, const void* scales, const void* zeros, const void* x, const void* bias,
+                               void* y, int N, int K, int variant, void* stream);
+
+/* ---- on-device dequantisation to fp32 [N][K] (no reference C symbol; the values of src/paia_gemv/quant.py:16-17,
+ *      34-38 and quant_host.h:82-85,106-111). out 16-byte aligned. ---------------------------------------------- */
+PAIA_API int paia_dequant_fp8(const void* Wq, const void* scale, void* out, int N, int K, void* stream);
+PAIA_API int paia_dequant_int4(const void* Wq, const void* scales, void* out, int N, int K, void* stream);
+PAIA_API int paia_dequant_int4_zp(const void* Wq, const void* scales, const void* zeros, void* out, int N, int K,
+                                  void* stream);
+
+/* no reference counterpart (the reference picks variants in Python from src/tuned/<platform>.json,
+ * paia-bench/bench/ops/ours_bf16.py:32-38): the library's per-shape variant for kind 0 BF16, 1 FP8, 2 INT4 (both
+ * INT4 formats). Always returns a valid index of that kind's table. */
+PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
+
+/* no reference counterpart: a human-readable build tag */
+PAIA_API const char* paia_gemv_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,170 @@
+// Device helpers for the gfx950 (CDNA4) GEMV kernels: buffer-resource loads, format decode + dot products on the
+// VALU, wave64 reductions, and the bf16 round-to-nearest-even used by every epilogue.
+//
+// Everything here is written for wave64 gfx950 only. Weight rows are read with raw buffer loads whose descriptor is
+// bounded to the row, so loads past the end of a row (K tails, rows >= N) return zeros without a branch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace paia {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------------------------------------
+// weight formats
+// ---------------------------------------------------------------------------------------------------------------
+enum Fmt : int {
+    kBF16 = 0,   // W bf16 [N][K]
+    kFP8 = 1,    // W e4m3fn [N][K], fp32 scale per row
+    kI4 = 2,     // W uint4 [N][K/2] (z = 8), fp16 scale [N][K/128]         (reference format)
+    kI4ZP = 3,   // W uint4 [N][K/2], bf16 scale [N][G], 4-bit zero [N][ceil(G/2)] (asymmetric format)
+};
+
+// Per format: weight columns covered by one 16-byte load, and how many 16-byte LDS x vectors (8 bf16 each) they need.
+template <int F> struct FmtInfo;
+template <> struct FmtInfo<kBF16> { static constexpr int kColsPer16B = 8;  static constexpr int kXQ = 1; };
+template <> struct FmtInfo<kFP8>  { static constexpr int kColsPer16B = 16; static constexpr int kXQ = 2; };
+template <> struct FmtInfo<kI4>   { static constexpr int kColsPer16B = 32; static constexpr int kXQ = 4; };
+template <> struct FmtInfo<kI4ZP> { static constexpr int kColsPer16B = 32; static constexpr int kXQ = 4; };
+
+// A "chunk" is what one wave reads from one weight row with one 16-byte load per lane: 1 KiB.
+constexpr int kWave = 64;
+constexpr int kChunkBytes = kWave * 16;
+
+// ---------------------------------------------------------------------------------------------------------------
+// buffer resources (gfx9 family: dword3 = 0x00020000, raw buffer, no swizzle)
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+
+// aux = cache policy: 0 default, 2 = nt (streaming; the weights are read exactly once per call).
+template <int AUX>
+__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+}
+__device__ __forceinline__ uint32_t ld_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t ld_u8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// arithmetic
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc)
+{
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h16)
+{
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h16);
+}
+
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Two e4m3fn bytes (byte pair HI of word w) -> two bf16, exact for every finite code (OCP conversion on gfx950).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
+// 8 bf16 weights (one 16-byte load) dot 8 x values.
+__device__ __forceinline__ float dot_bf16_16B(const u32x4 w, const u32x4 x, float acc)
+{
+    acc = dot2_bf16(w.x, x.x, acc);
+    acc = dot2_bf16(w.y, x.y, acc);
+    acc = dot2_bf16(w.z, x.z, acc);
+    acc = dot2_bf16(w.w, x.w, acc);
+    return acc;
+}
+
+// 16 e4m3 weights (one 16-byte load) dot 16 x values (x0 = columns 0..7, x1 = columns 8..15).
+__device__ __forceinline__ float fp8_word_dot(uint32_t w, uint32_t xa, uint32_t xb, float acc)
+{
+    acc = dot2_bf16(fp8x2_to_bf16x2<false>(w), xa, acc);
+    acc = dot2_bf16(fp8x2_to_bf16x2<true>(w), xb, acc);
+    return acc;
+}
+__device__ __forceinline__ float dot_fp8_16B(const u32x4 w, const u32x4 x0, const u32x4 x1, float acc)
+{
+    acc = fp8_word_dot(w.x, x0.x, x0.y, acc);
+    acc = fp8_word_dot(w.y, x0.z, x0.w, acc);
+    acc = fp8_word_dot(w.z, x1.x, x1.y, acc);
+    acc = fp8_word_dot(w.w, x1.z, x1.w, acc);
+    return acc;
+}
+
+// INT4: eight nibbles of one word (weights k..k+7, nibble j = weight k+j) against 8 x values staged in LDS in the
+// order (x0,x4),(x1,x5),(x2,x6),(x3,x7). Each nibble pair is turned into two bf16 (128 + q) by masking it into the
+// low mantissa bits of 0x4300 (bf16 128.0, whose ulp is 1), so sum (128+q) x = sum q x + 128 sum x; the caller
+// removes the 128 sum x term (and the zero point) with the per-segment x sums.
+__device__ __forceinline__ float i4_word_dot(uint32_t w, const u32x4 x, float acc)
+{
+    constexpr uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;
+    acc = dot2_bf16((w & kMask) | kMagic, x.x, acc);
+    acc = dot2_bf16(((w >> 4) & kMask) | kMagic, x.y, acc);
+    acc = dot2_bf16(((w >> 8) & kMask) | kMagic, x.z, acc);
+    acc = dot2_bf16(((w >> 12) & kMask) | kMagic, x.w, acc);
+    return acc;
+}
+__device__ __forceinline__ float dot_i4_16B(const u32x4 w, const u32x4 x0, const u32x4 x1, const u32x4 x2,
+                                            const u32x4 x3)
+{
+    float d = i4_word_dot(w.x, x0, 0.0f);
+    d = i4_word_dot(w.y, x1, d);
+    d = i4_word_dot(w.z, x2, d);
+    d = i4_word_dot(w.w, x3, d);
+    return d;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// wave64 reduction: DPP within each row of 16 lanes, then the four row sums via readlane (result is wave-uniform).
+// The order of additions is fixed, so results are bitwise reproducible.
+// ---------------------------------------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);   // row_ror:4
+    v += dpp_f32<0x128>(v);   // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+// Sum over the 4 lanes of a quad (result in every lane of the quad).
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    return v;
+}
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+}  // namespace paia

@@ -1,0 +1,38 @@
+// Process-wide device facts for grid sizing. Queried once (first launch) and cached; no allocation, no sync.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+
+#include "gemv_kernel.h"
+#include "paia_gemv.h"
+
+namespace paia {
+
+DeviceFacts device_facts()
+{
+    static std::atomic<int> cus{0}, lds{0};
+    DeviceFacts f;
+    f.cus = cus.load(std::memory_order_relaxed);
+    f.lds_per_cu = lds.load(std::memory_order_relaxed);
+    if (f.cus == 0) {
+        int dev = 0, n = 0, l = 0;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+            if (hipDeviceGetAttribute(&l, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess) l = 0;
+        }
+        f.cus = n > 0 ? n : 256;
+        f.lds_per_cu = l > 0 ? l : 65536;
+        cus.store(f.cus, std::memory_order_relaxed);
+        lds.store(f.lds_per_cu, std::memory_order_relaxed);
+    }
+    return f;
+}
+
+}  // namespace paia
+
+extern "C" {
+
+// Build identification (no reference counterpart): lets callers check which library they loaded.
+const char* paia_gemv_build_info() { return "paia_gemv gfx950 HIP build (wave64, LDS-staged x, buffer-load streaming)"; }
+
+}  // extern "C"

@@ -1,0 +1,286 @@
+// torch.library custom ops over libpaia_gemv.so: the thin PyTorch-ROCm layer of the paia_gemv package.
+//
+// Namespace torch.ops.paia_gemv. Each op validates its tensors, resolves the variant (-1 = the library's per-shape
+// pick), and calls the C ABI on torch's current HIP stream of the operand's device, so the ops compose with torch
+// streams and HIP graph capture. Functional ops allocate their output; the *_out ops write a caller-given output and
+// allocate nothing. Meta kernels give shapes for tracing.
+//
+// The reference reaches its kernels through ctypes only (src/paia_gemv/loader.py:28-99); these ops are the additional
+// Tensor-level surface (same semantics, same return-code errors surfaced as RuntimeError).
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <cstdint>
+#include <optional>
+
+#include "paia_gemv.h"
+
+namespace {
+
+enum Kind { kBF16 = 0, kFP8 = 1, kINT4 = 2 };
+
+void check_rc(int rc, const char* what)
+{
+    TORCH_CHECK(rc == 0, what, " failed with code ", rc,
+                " (-1 bad variant, -2 bad shape/alignment, >0 hipError_t)");
+}
+
+void* stream_of(const at::Tensor& t)
+{
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+int64_t x_len(const at::Tensor& x)
+{
+    TORCH_CHECK(x.dim() == 1 || (x.dim() == 2 && x.size(0) == 1), "x must be [K] or [1, K] (M = 1 only)");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16");
+    TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+    return x.size(-1);
+}
+
+std::vector<int64_t> y_shape(const at::Tensor& x, int64_t N)
+{
+    if (x.dim() == 2) return {1, N};
+    return {N};
+}
+
+void check_out(const at::Tensor& out, const at::Tensor& x, int64_t N)
+{
+    TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.is_contiguous() && out.numel() == N,
+                "out must be a contiguous bfloat16 tensor with N elements");
+    TORCH_CHECK(out.device() == x.device(), "out must be on the device of x");
+}
+
+const void* opt_ptr(const std::optional<at::Tensor>& t, int64_t N)
+{
+    if (!t.has_value()) return nullptr;
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16 && t->is_contiguous() && t->numel() == N,
+                "bias must be a contiguous bfloat16 tensor with N elements");
+    return t->data_ptr();
+}
+
+int pick(int64_t variant, int kind, int64_t N, int64_t K)
+{
+    return variant >= 0 ? (int)variant : paia_gemv_pick_variant(kind, (int)N, (int)K);
+}
+
+// -------------------------------------------------------------------------------------------------------------
+void gemv_bf16_out(const at::Tensor& W, const at::Tensor& x, const std::optional<at::Tensor>& bias, int64_t variant,
+                   at::Tensor& out)
+{
+    TORCH_CHECK(W.dim() == 2 && W.scalar_type() == at::kBFloat16 && W.is_contiguous(), "W must be bf16 [N, K]");
+    const int64_t N = W.size(0), K = W.size(1);
+    TORCH_CHECK(x_len(x) == K, "x length must equal K");
+    check_out(out, x, N);
+    c10::DeviceGuard g(W.device());
+    check_rc(paia_gemv_bf16_bias(W.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(), (int)N, (int)K,
+                                 pick(variant, kBF16, N, K), stream_of(W)),
+             "paia_gemv_bf16");
+}
+at::Tensor gemv_bf16(const at::Tensor& W, const at::Tensor& x, const std::optional<at::Tensor>& bias, int64_t variant)
+{
+    at::Tensor out = at::empty(y_shape(x, W.size(0)), x.options());
+    gemv_bf16_out(W, x, bias, variant, out);
+    return out;
+}
+
+void gemv_fp8_out(const at::Tensor& Wq, const at::Tensor& scale, const at::Tensor& x,
+                  const std::optional<at::Tensor>& bias, int64_t variant, at::Tensor& out)
+{
+    TORCH_CHECK(Wq.dim() == 2 && Wq.element_size() == 1 && Wq.is_contiguous(), "Wq must be 1-byte e4m3 [N, K]");
+    const int64_t N = Wq.size(0), K = Wq.size(1);
+    TORCH_CHECK(scale.scalar_type() == at::kFloat && scale.numel() == N && scale.is_contiguous(), "scale: fp32 [N]");
+    TORCH_CHECK(x_len(x) == K, "x length must equal K");
+    check_out(out, x, N);
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_gemv_fp8_bias(Wq.data_ptr(), scale.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(),
+                                (int)N, (int)K, pick(variant, kFP8, N, K), stream_of(Wq)),
+             "paia_gemv_fp8");
+}
+at::Tensor gemv_fp8(const at::Tensor& Wq, const at::Tensor& scale, const at::Tensor& x,
+                    const std::optional<at::Tensor>& bias, int64_t variant)
+{
+    at::Tensor out = at::empty(y_shape(x, Wq.size(0)), x.options());
+    gemv_fp8_out(Wq, scale, x, bias, variant, out);
+    return out;
+}
+
+// Packed INT4 weights: uint8 [N, K/2] or int32 [N, K/8] (the same bytes on a little-endian machine).
+int64_t int4_K(const at::Tensor& Wq)
+{
+    TORCH_CHECK(Wq.dim() == 2 && Wq.is_contiguous(), "Wq must be a contiguous 2-D tensor");
+    if (Wq.scalar_type() == at::kByte) return Wq.size(1) * 2;
+    TORCH_CHECK(Wq.scalar_type() == at::kInt, "Wq must be uint8 [N, K/2] or int32 [N, K/8]");
+    return Wq.size(1) * 8;
+}
+
+void gemv_int4_out(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& x, int64_t variant,
+                   at::Tensor& out)
+{
+    const int64_t N = Wq.size(0), K = int4_K(Wq);
+    TORCH_CHECK(scales.scalar_type() == at::kHalf && scales.is_contiguous() && scales.numel() == N * (K / 128),
+                "scales: fp16 [N, K/128]");
+    TORCH_CHECK(x_len(x) == K, "x length must equal K");
+    check_out(out, x, N);
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_gemv_int4(Wq.data_ptr(), scales.data_ptr(), x.data_ptr(), out.data_ptr(), (int)N, (int)K,
+                            pick(variant, kINT4, N, K), stream_of(Wq)),
+             "paia_gemv_int4");
+}
+at::Tensor gemv_int4(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& x, int64_t variant)
+{
+    at::Tensor out = at::empty(y_shape(x, Wq.size(0)), x.options());
+    gemv_int4_out(Wq, scales, x, variant, out);
+    return out;
+}
+
+void gemv_int4_zp_out(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& zeros, const at::Tensor& x,
+                      const std::optional<at::Tensor>& bias, int64_t variant, at::Tensor& out)
+{
+    const int64_t N = Wq.size(0), K = int4_K(Wq), G = K / 128;
+    TORCH_CHECK(scales.scalar_type() == at::kBFloat16 && scales.is_contiguous() && scales.numel() == N * G,
+                "scales: bf16 [N, K/128]");
+    TORCH_CHECK(zeros.scalar_type() == at::kByte && zeros.is_contiguous() && zeros.numel() == N * ((G + 1) / 2),
+                "zeros: uint8 [N, ceil(K/256)] (two 4-bit zero points per byte along the groups)");
+    TORCH_CHECK(x_len(x) == K, "x length must equal K");
+    check_out(out, x, N);
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_gemv_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), x.data_ptr(), opt_ptr(bias, N),
+                               out.data_ptr(), (int)N, (int)K, pick(variant, kINT4, N, K), stream_of(Wq)),
+             "paia_gemv_int4_zp");
+}
+at::Tensor gemv_int4_zp(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& zeros, const at::Tensor& x,
+                        const std::optional<at::Tensor>& bias, int64_t variant)
+{
+    at::Tensor out = at::empty(y_shape(x, Wq.size(0)), x.options());
+    gemv_int4_zp_out(Wq, scales, zeros, x, bias, variant, out);
+    return out;
+}
+
+at::Tensor dequant_fp8(const at::Tensor& Wq, const at::Tensor& scale)
+{
+    TORCH_CHECK(Wq.dim() == 2 && Wq.element_size() == 1 && Wq.is_contiguous(), "Wq must be 1-byte e4m3 [N, K]");
+    const int64_t N = Wq.size(0), K = Wq.size(1);
+    TORCH_CHECK(scale.scalar_type() == at::kFloat && scale.numel() == N && scale.is_contiguous(), "scale: fp32 [N]");
+    at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_dequant_fp8(Wq.data_ptr(), scale.data_ptr(), out.data_ptr(), (int)N, (int)K, stream_of(Wq)),
+             "paia_dequant_fp8");
+    return out;
+}
+
+at::Tensor dequant_int4(const at::Tensor& Wq, const at::Tensor& scales)
+{
+    const int64_t N = Wq.size(0), K = int4_K(Wq);
+    TORCH_CHECK(scales.scalar_type() == at::kHalf && scales.is_contiguous() && scales.numel() == N * (K / 128),
+                "scales: fp16 [N, K/128]");
+    at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_dequant_int4(Wq.data_ptr(), scales.data_ptr(), out.data_ptr(), (int)N, (int)K, stream_of(Wq)),
+             "paia_dequant_int4");
+    return out;
+}
+
+at::Tensor dequant_int4_zp(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& zeros)
+{
+    const int64_t N = Wq.size(0), K = int4_K(Wq), G = K / 128;
+    TORCH_CHECK(scales.scalar_type() == at::kBFloat16 && scales.is_contiguous() && scales.numel() == N * G,
+                "scales: bf16 [N, K/128]");
+    TORCH_CHECK(zeros.scalar_type() == at::kByte && zeros.is_contiguous() && zeros.numel() == N * ((G + 1) / 2),
+                "zeros: uint8 [N, ceil(K/256)]");
+    at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
+    c10::DeviceGuard g(Wq.device());
+    check_rc(paia_dequant_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), out.data_ptr(), (int)N, (int)K,
+                                  stream_of(Wq)),
+             "paia_dequant_int4_zp");
+    return out;
+}
+
+// ---- Meta (shape-only) kernels ------------------------------------------------------------------------------
+at::Tensor gemv_bf16_meta(const at::Tensor& W, const at::Tensor& x, const std::optional<at::Tensor>&, int64_t)
+{
+    return at::empty(y_shape(x, W.size(0)), x.options());
+}
+at::Tensor gemv_fp8_meta(const at::Tensor& Wq, const at::Tensor&, const at::Tensor& x, const std::optional<at::Tensor>&,
+                         int64_t)
+{
+    return at::empty(y_shape(x, Wq.size(0)), x.options());
+}
+at::Tensor gemv_int4_meta(const at::Tensor& Wq, const at::Tensor&, const at::Tensor& x, int64_t)
+{
+    return at::empty(y_shape(x, Wq.size(0)), x.options());
+}
+at::Tensor gemv_int4_zp_meta(const at::Tensor& Wq, const at::Tensor&, const at::Tensor&, const at::Tensor& x,
+                             const std::optional<at::Tensor>&, int64_t)
+{
+    return at::empty(y_shape(x, Wq.size(0)), x.options());
+}
+at::Tensor dequant_fp8_meta(const at::Tensor& Wq, const at::Tensor&)
+{
+    return at::empty({Wq.size(0), Wq.size(1)}, Wq.options().dtype(at::kFloat));
+}
+at::Tensor dequant_int4_meta(const at::Tensor& Wq, const at::Tensor&)
+{
+    return at::empty({Wq.size(0), int4_K(Wq)}, Wq.options().dtype(at::kFloat));
+}
+at::Tensor dequant_int4_zp_meta(const at::Tensor& Wq, const at::Tensor&, const at::Tensor&)
+{
+    return at::empty({Wq.size(0), int4_K(Wq)}, Wq.options().dtype(at::kFloat));
+}
+void out_meta_bf16(const at::Tensor&, const at::Tensor&, const std::optional<at::Tensor>&, int64_t, at::Tensor&) {}
+void out_meta_fp8(const at::Tensor&, const at::Tensor&, const at::Tensor&, const std::optional<at::Tensor>&, int64_t,
+                  at::Tensor&) {}
+void out_meta_int4(const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t, at::Tensor&) {}
+void out_meta_int4_zp(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                      const std::optional<at::Tensor>&, int64_t, at::Tensor&) {}
+
+}  // namespace
+
+TORCH_LIBRARY(paia_gemv, m)
+{
+    m.def("gemv_bf16(Tensor W, Tensor x, Tensor? bias=None, int variant=-1) -> Tensor");
+    m.def("gemv_bf16_out(Tensor W, Tensor x, Tensor? bias, int variant, Tensor(a!) out) -> ()");
+    m.def("gemv_fp8(Tensor Wq, Tensor scale, Tensor x, Tensor? bias=None, int variant=-1) -> Tensor");
+    m.def("gemv_fp8_out(Tensor Wq, Tensor scale, Tensor x, Tensor? bias, int variant, Tensor(a!) out) -> ()");
+    m.def("gemv_int4(Tensor Wq, Tensor scales, Tensor x, int variant=-1) -> Tensor");
+    m.def("gemv_int4_out(Tensor Wq, Tensor scales, Tensor x, int variant, Tensor(a!) out) -> ()");
+    m.def("gemv_int4_zp(Tensor Wq, Tensor scales, Tensor zeros, Tensor x, Tensor? bias=None, int variant=-1) -> Tensor");
+    m.def("gemv_int4_zp_out(Tensor Wq, Tensor scales, Tensor zeros, Tensor x, Tensor? bias, int variant, "
+          "Tensor(a!) out) -> ()");
+    m.def("dequant_fp8(Tensor Wq, Tensor scale) -> Tensor");
+    m.def("dequant_int4(Tensor Wq, Tensor scales) -> Tensor");
+    m.def("dequant_int4_zp(Tensor Wq, Tensor scales, Tensor zeros) -> Tensor");
+}
+
+// torch on ROCm dispatches HIP tensors under the CUDA key.
+TORCH_LIBRARY_IMPL(paia_gemv, CUDA, m)
+{
+    m.impl("gemv_bf16", &gemv_bf16);
+    m.impl("gemv_bf16_out", &gemv_bf16_out);
+    m.impl("gemv_fp8", &gemv_fp8);
+    m.impl("gemv_fp8_out", &gemv_fp8_out);
+    m.impl("gemv_int4", &gemv_int4);
+    m.impl("gemv_int4_out", &gemv_int4_out);
+    m.impl("gemv_int4_zp", &gemv_int4_zp);
+    m.impl("gemv_int4_zp_out", &gemv_int4_zp_out);
+    m.impl("dequant_fp8", &dequant_fp8);
+    m.impl("dequant_int4", &dequant_int4);
+    m.impl("dequant_int4_zp", &dequant_int4_zp);
+}
+
+TORCH_LIBRARY_IMPL(paia_gemv, Meta, m)
+{
+    m.impl("gemv_bf16", &gemv_bf16_meta);
+    m.impl("gemv_bf16_out", &out_meta_bf16);
+    m.impl("gemv_fp8", &gemv_fp8_meta);
+    m.impl("gemv_fp8_out", &out_meta_fp8);
+    m.impl("gemv_int4", &gemv_int4_meta);
+    m.impl("gemv_int4_out", &out_meta_int4);
+    m.impl("gemv_int4_zp", &gemv_int4_zp_meta);
+    m.impl("gemv_int4_zp_out", &out_meta_int4_zp);
+    m.impl("dequant_fp8", &dequant_fp8_meta);
+    m.impl("dequant_int4", &dequant_int4_meta);
+    m.impl("dequant_int4_zp", &dequant_int4_zp_meta);
+}

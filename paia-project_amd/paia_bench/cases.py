@@ -1,0 +1,137 @@
+"""One GEMV configuration on the device: n_copies operand sets for cache-defeating rotation and a launch closure.
+
+Copy 0 holds the seeded BASELINE operands (paia_bench.inputs), the one checked for correctness before any timing
+(as paia-bench/bench/run.py:236-240 gates cells). Copies 1.. hold random codes of the same format generated on the
+device: the kernels have no data-dependent control flow, so timing does not depend on the values
+(paia-bench/bench/ops/ours_quant.py:3-6 uses the same convention).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from paia_gemv.shapes import gemv_bytes
+
+from .inputs import as_numpy, make_operands, to_device
+
+
+def kind_of(fmt: str) -> str:
+    return "int4" if fmt.startswith("int4") else fmt
+
+
+class GemvCase:
+    def __init__(self, lib, fmt: str, N: int, K: int, bias: bool = False, variant: int | None = None,
+                 mode: str = "fused", name: str | None = None):
+        self.lib, self.fmt, self.N, self.K, self.bias, self.mode = lib, fmt, N, K, bias, mode
+        self.name = name or f"{fmt}_{N}x{K}"
+        self.variant = lib.pick_variant(kind_of(fmt), N, K) if variant is None else int(variant)
+        self.copies: list = []
+        self.ptrs: list = []
+        self.scratch = None
+        self.ops0 = None
+
+    # ---- accounting --------------------------------------------------------------------------------------
+    def bytes(self) -> dict:
+        return gemv_bytes(self.fmt, self.N, self.K, self.bias)
+
+    def footprint(self) -> int:
+        return self.bytes()["total"]
+
+    # ---- operands ----------------------------------------------------------------------------------------
+    def _random_copy(self, dev, g):
+        N, K, G = self.N, self.K, self.K // 128
+        c = {"N": N, "K": K, "x": torch.randn(K, device=dev, generator=g).to(torch.bfloat16)}
+        u8 = lambda *s: torch.randint(0, 256, s, device=dev, generator=g, dtype=torch.uint8)
+        if self.fmt == "bf16":
+            c["W"] = (0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16)
+        elif self.fmt == "fp8":
+            c["Wq"] = u8(N, K)
+            c["scale"] = torch.rand(N, device=dev, generator=g).mul_(0.01).add_(1e-3)
+        elif self.fmt == "int4":
+            c["Wq"] = u8(N, K // 2)
+            c["scales"] = torch.rand(N, G, device=dev, generator=g).mul_(0.01).add_(1e-3).half()
+        else:
+            c["Wq"] = u8(N, K // 2)
+            c["scales"] = torch.rand(N, G, device=dev, generator=g).mul_(0.01).add_(1e-3).bfloat16()
+            c["zeros"] = u8(N, (G + 1) // 2)
+        c["bias"] = (0.02 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16) if self.bias else None
+        return c
+
+    def build(self, n_copies: int, device="cuda", seed: int = 1234):
+        dev = torch.device(device)
+        self.ops0 = make_operands(self.fmt, self.N, self.K, bias=self.bias)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.copies = [to_device(self.ops0, dev)] + [self._random_copy(dev, g) for _ in range(n_copies - 1)]
+        for c in self.copies:
+            c["y"] = torch.empty(self.N, dtype=torch.bfloat16, device=dev)
+        if self.mode == "unfused":
+            self.scratch = torch.empty(self.N * self.K, dtype=torch.bfloat16, device=dev)
+        self.ptrs = [self._ptrs(c) for c in self.copies]
+        return self
+
+    @staticmethod
+    def _ptr(t):
+        return None if t is None else t.data_ptr()
+
+    def _ptrs(self, c):
+        p = self._ptr
+        if self.fmt == "bf16":
+            return (p(c["W"]), p(c["x"]), p(c["bias"]), p(c["y"]))
+        if self.fmt == "fp8":
+            return (p(c["Wq"]), p(c["scale"]), p(c["x"]), p(c["bias"]), p(c["y"]))
+        if self.fmt == "int4":
+            return (p(c["Wq"]), p(c["scales"]), p(c["x"]), p(c["y"]))
+        return (p(c["Wq"]), p(c["scales"]), p(c["zeros"]), p(c["x"]), p(c["bias"]), p(c["y"]))
+
+    # ---- launch ------------------------------------------------------------------------------------------
+    def call(self, i: int, stream=None):
+        L, N, K, v = self.lib, self.N, self.K, self.variant
+        P = self.ptrs[i]
+        if self.fmt == "bf16":
+            W, x, b, y = P
+            if b is None:
+                L.bf16(W, x, y, N, K, v, stream)
+            else:
+                L.bf16_bias(W, x, b, y, N, K, v, stream)
+        elif self.fmt == "fp8":
+            Wq, s, x, b, y = P
+            if b is None:
+                L.fp8(Wq, s, x, y, N, K, v, stream)
+            else:
+                L.fp8_bias(Wq, s, x, b, y, N, K, v, stream)
+        elif self.fmt == "int4":
+            Wq, s, x, y = P
+            if self.mode == "fused":
+                L.int4(Wq, s, x, y, N, K, v, stream)
+            elif self.mode == "naive":
+                L.int4_naive(Wq, s, x, y, N, K, stream)
+            else:
+                L.int4_unfused(Wq, s, x, y, self.scratch.data_ptr(), N, K, stream)
+        else:
+            Wq, s, z, x, b, y = P
+            L.int4_zp(Wq, s, z, x, b, y, N, K, v, stream)
+        return self.copies[i]["y"]
+
+    # ---- correctness gate on copy 0 ----------------------------------------------------------------------
+    def check(self, oracle, rows=None, rtol=1e-2, atol=1e-2) -> dict:
+        """Compare copy 0 with the CPU oracle (fp64, on `rows` or all rows): BASELINE gate and reference gate."""
+        y = self.call(0)
+        torch.cuda.synchronize()
+        yb = y.cpu().view(torch.int16).numpy().view(np.uint16)
+        a = as_numpy(self.ops0)
+        b = a.get("bias")
+        if self.fmt == "bf16":
+            ref = oracle.gemv_bf16_f64(a["W"], a["x"], b, rows)
+        elif self.fmt == "fp8":
+            ref = oracle.gemv_fp8_f64(a["Wq"], a["scale"], a["x"], b, rows)
+        elif self.fmt == "int4":
+            ref = oracle.gemv_int4_f64(a["Wq"], a["scales"], a["x"], rows)
+        else:
+            ref = oracle.gemv_int4_zp_f64(a["Wq"], a["scales"], a["zeros"], a["x"], b, rows)
+        got = yb if rows is None else yb[np.asarray(rows)]
+        ok, excess, rel = oracle.close_to_ref(got, ref, rtol, atol)
+        return {"ok": bool(ok and rel < 2e-2), "rel_err": rel, "worst_excess": excess,
+                "rows_checked": int(len(got))}
+
+    def free(self):
+        self.copies, self.ptrs, self.scratch = [], [], None

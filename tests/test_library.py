@@ -1,0 +1,150 @@
+"""The drop-in boundary without a GPU: libpaia_gemv.so loads, exports every symbol include/paia_gemv.h declares,
+keeps the reference's variant tuples and return-code contract, and the torch ops are registered with correct
+shape (Meta) behaviour. Nothing here launches a kernel: every call below returns from the host-side checks."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "paia_gemv.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"PAIA_API\s+[\w\s\*]*?\b(paia_\w+)\s*\(", text)))
+
+
+def test_header_declares_reference_symbols():
+    """The eleven reference entry points (src/paia_gemv/gemv_bf16.cu:35-55, gemv_quant.cu:59-99) are all declared."""
+    ref = {"paia_gemv_bf16_variant_count", "paia_gemv_bf16_variant_info", "paia_gemv_bf16",
+           "paia_gemv_fp8_variant_count", "paia_gemv_fp8_variant_info", "paia_gemv_fp8",
+           "paia_gemv_int4_variant_count", "paia_gemv_int4_variant_info", "paia_gemv_int4",
+           "paia_gemv_int4_naive", "paia_gemv_int4_unfused"}
+    assert ref <= set(declared_symbols())
+
+
+def test_library_exports_every_declared_symbol(gemv_lib):
+    raw = ctypes.CDLL(gemv_lib.path)
+    missing = [s for s in declared_symbols() if not hasattr(raw, s)]
+    assert not missing, missing
+
+
+def test_exports_are_exactly_the_header(gemv_lib):
+    """-fvisibility=hidden: the library's dynamic symbol table holds the header's entry points and nothing else."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", gemv_lib.path], capture_output=True, text=True).stdout
+    exported = sorted({l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith("paia_")})
+    assert exported == declared_symbols()
+
+
+def test_variant_tables_hold_harness_defaults(gemv_lib):
+    """paia-bench/bench/ops/ours_bf16.py:22 and ours_quant.py:19 look these tuples up by value (KeyError otherwise)."""
+    def has(vs, want):
+        return any(all(v[k] == want[k] for k in "RUWSH") for v in vs)
+    assert gemv_lib.n_variants == 96 and len(gemv_lib.variants_fp8) == 36 and len(gemv_lib.variants_int4) == 48
+    assert has(gemv_lib.variants, {"R": 2, "U": 4, "W": 4, "S": 0, "H": 1})
+    assert has(gemv_lib.variants_fp8, {"R": 2, "U": 2, "W": 4, "S": 0, "H": 1})
+    assert has(gemv_lib.variants_int4, {"R": 4, "U": 2, "W": 4, "S": 0, "H": 1})
+    keys = {(v["R"], v["U"], v["W"], v["S"], v["H"]) for v in gemv_lib.variants}
+    assert len(keys) == 96                                               # tuples are unique
+    for kind in ("bf16", "fp8", "int4"):
+        n = {"bf16": 96, "fp8": 36, "int4": 48}[kind]
+        for N, K in [(4096, 4096), (6144, 4096), (3584, 18944), (1, 128)]:
+            assert 0 <= gemv_lib.pick_variant(kind, N, K) < n
+
+
+def test_variant_info_rejects_out_of_range(gemv_lib):
+    raw = gemv_lib._lib
+    a = [ctypes.c_int() for _ in range(5)]
+    assert raw.paia_gemv_bf16_variant_info(96, *map(ctypes.byref, a)) == -1
+    assert raw.paia_gemv_bf16_variant_info(-1, *map(ctypes.byref, a)) == -1
+
+
+def test_contract_return_codes_without_launch(gemv_lib):
+    """Host-side checks return before any launch: -1 bad variant, -2 bad shape/alignment
+    (src/paia_gemv/gemv_bf16.cu:50-51, gemv_quant.cu:66,75,81,89; gemv_bf16_check.cu:375-376,474-476)."""
+    L = gemv_lib._lib
+    A = 1 << 20            # a 16-byte-aligned fake address: never dereferenced, every call fails its checks first
+    assert L.paia_gemv_bf16(A, A, A, 4, 12, 0, None) == -2            # K % 8
+    assert L.paia_gemv_bf16(A, A, A, 0, 16, 0, None) == -2            # N <= 0
+    assert L.paia_gemv_bf16(A + 2, A, A, 4, 16, 0, None) == -2        # W not 16-byte aligned
+    assert L.paia_gemv_bf16(A, A, A + 2, 4, 16, 0, None) == -2        # y not 16-byte aligned
+    assert L.paia_gemv_bf16(A, A, A, 4, 16, 96, None) == -1           # variant out of range
+    assert L.paia_gemv_fp8(A, A, A, A, 4, 24, 0, None) == -2          # K % 16
+    assert L.paia_gemv_fp8(A, A + 2, A, A, 4, 32, 0, None) == -2      # scale not 4-byte aligned
+    assert L.paia_gemv_fp8(A, A, A, A, 4, 32, 36, None) == -1
+    assert L.paia_gemv_int4(A, A, A, A, 4, 64, 0, None) == -2         # K % 128
+    assert L.paia_gemv_int4(A, A + 1, A, A, 4, 128, 0, None) == -2    # scales not 2-byte aligned
+    assert L.paia_gemv_int4(A, A, A, A, 4, 128, 48, None) == -1
+    assert L.paia_gemv_int4_naive(A, A, A, A, 4, 64, None) == -2
+    assert L.paia_gemv_int4_unfused(A, A, A, A, A + 8, 4, 128, None) == -2   # scratch alignment
+    assert L.paia_gemv_int4_zp(A, A, None, A, None, A, 4, 128, 0, None) == -2  # zeros missing
+    assert L.paia_gemv_int4_zp(A, A, A, A, A + 1, A, 4, 128, 0, None) == -2    # bias alignment
+    assert L.paia_gemv_bf16_bias(A, A, A + 1, A, 4, 16, 0, None) == -2
+    assert L.paia_dequant_fp8(A, A, A, 4, 8, None) == -2
+    assert L.paia_dequant_int4(A, A, A + 4, 4, 128, None) == -2
+    assert L.paia_dequant_int4_zp(A, A, None, A, 4, 128, None) == -2
+    # LDS limit of the gfx950 design: x is staged in 64 KiB
+    assert L.paia_gemv_bf16(A, A, A, 4, 32768 + 8, 0, None) == -2
+    assert L.paia_gemv_int4(A, A, A, A, 4, 30720 + 128, 0, None) == -2
+
+
+def test_python_surface_matches_reference(gemv_lib):
+    """src/paia_gemv/loader.py:28-109: attributes and methods callers use."""
+    import paia_gemv
+    assert paia_gemv.load_lib() is paia_gemv.load_lib()
+    for name in ("bf16", "fp8", "int4", "int4_naive", "int4_unfused", "path", "n_variants", "variants",
+                 "variants_fp8", "variants_int4"):
+        assert hasattr(gemv_lib, name)
+    with pytest.raises(RuntimeError, match="-2"):
+        gemv_lib.bf16(1 << 20, 1 << 20, 1 << 20, 4, 12, 0, stream=0)
+    from paia_gemv import quant
+    for name in ("quantize_fp8_rowwise", "dequant_fp8", "quantize_int4_g128", "dequant_int4"):
+        assert callable(getattr(quant, name))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from paia_gemv import loader
+    monkeypatch.setenv("PAIA_GEMV_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(loader, "_PKG_ROOT", tmp_path)
+    with pytest.raises(FileNotFoundError):
+        loader.find_lib()
+
+
+def test_torch_ops_registered_and_meta_shapes():
+    from paia_gemv import ops
+    ops.load()
+    names = ["gemv_bf16", "gemv_bf16_out", "gemv_fp8", "gemv_fp8_out", "gemv_int4", "gemv_int4_out",
+             "gemv_int4_zp", "gemv_int4_zp_out", "dequant_fp8", "dequant_int4", "dequant_int4_zp"]
+    for n in names:
+        assert hasattr(torch.ops.paia_gemv, n)
+    m = torch.device("meta")
+    N, K = 48, 384
+    y = torch.ops.paia_gemv.gemv_bf16(torch.empty(N, K, dtype=torch.bfloat16, device=m),
+                                      torch.empty(1, K, dtype=torch.bfloat16, device=m), None, -1)
+    assert y.shape == (1, N) and y.dtype == torch.bfloat16
+    y = torch.ops.paia_gemv.gemv_int4_zp(torch.empty(N, K // 8, dtype=torch.int32, device=m),
+                                         torch.empty(N, 3, dtype=torch.bfloat16, device=m),
+                                         torch.empty(N, 2, dtype=torch.uint8, device=m),
+                                         torch.empty(K, dtype=torch.bfloat16, device=m), None, -1)
+    assert y.shape == (N,)
+    d = torch.ops.paia_gemv.dequant_int4(torch.empty(N, K // 2, dtype=torch.uint8, device=m),
+                                         torch.empty(N, 3, dtype=torch.float16, device=m))
+    assert d.shape == (N, K) and d.dtype == torch.float32
+
+
+def test_byte_accounting_matches_baseline_table():
+    """BASELINE.md section 2 figures (BF16 2NK+2K+2N; FP8 NK+4N+2K+2N; INT4 NK/2+2NG+NG/2+2K+2N; +2N with bias)."""
+    from paia_gemv.shapes import gemv_bytes
+    assert gemv_bytes("bf16", 4096, 4096)["total"] == 33_570_816
+    assert gemv_bytes("fp8", 6144, 4096)["total"] == 25_210_880
+    assert gemv_bytes("fp8", 28672, 4096)["total"] == 117_620_736
+    assert gemv_bytes("fp8", 4096, 14336)["total"] == 58_773_504
+    assert gemv_bytes("int4zp", 6144, 4096)["total"] == 13_094_912
+    assert gemv_bytes("int4zp", 4096, 14336)["total"] == 30_543_872
+    assert gemv_bytes("fp8", 4608, 3584, bias=True)["total"] == 16_559_104
+    assert gemv_bytes("int4zp", 3584, 18944)["total"] == 35_318_784
+    assert gemv_bytes("bf16", 152064, 3584)["total"] == 1_090_306_048
