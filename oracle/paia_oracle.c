@@ -156,12 +156,18 @@ void po_quantize_int4_g128(const float* W, int N, int K, uint8_t* packed, uint16
 
 static inline unsigned nibble_at(const uint8_t* row, int k) { return (row[k >> 1] >> ((k & 1) * 4)) & 0xFu; }
 
-/* Follows src/paia_gemv/quant.py:16-17 and quant_host.h:82-85: float(e4m3) * scale[n], one fp32 product. */
+/* Follows src/paia_gemv/quant.py:16-17 and quant_host.h:82-85: float(e4m3) * scale[n], one fp32 product.
+ * (The 256 code values are taken from po_e4m3_to_f32 once.) */
 void po_dequant_fp8(const uint8_t* q, const float* scale, int N, int K, float* out)
 {
-    for (int n = 0; n < N; ++n)
-        for (int k = 0; k < K; ++k)
-            out[(size_t)n * K + k] = po_e4m3_to_f32(q[(size_t)n * K + k]) * scale[n];
+    float tab[256];
+    for (int c = 0; c < 256; ++c) tab[c] = po_e4m3_to_f32((uint8_t)c);
+    for (int n = 0; n < N; ++n) {
+        const uint8_t* qr = q + (size_t)n * (size_t)K;
+        float* o = out + (size_t)n * (size_t)K;
+        const float s = scale[n];
+        for (int k = 0; k < K; ++k) o[k] = tab[qr[k]] * s;
+    }
 }
 
 /* Follows src/paia_gemv/quant.py:34-38 and quant_host.h:106-111: (n - 8) * float(s16) (exact in fp32). */

@@ -6,6 +6,7 @@
 Outputs (git-ignored, shipped with the tree):
     paia-project_amd/build/libpaia_gemv.so          C ABI declared in include/paia_gemv.h
     paia-project_amd/build/libpaia_gemv_torch.so    torch.ops.paia_gemv.* (links libpaia_gemv.so via $ORIGIN)
+    paia-project_amd/build/libpaia_probe.so         measurement kernels of the benchmark harness
 
 Replaces src/paia_gemv/build.sh (nvcc, static cudart). Every HIP source is compiled for gfx950 only, with packed
 fp32 VALU instructions disabled (-Xclang -target-feature -Xclang -packed-fp32-ops); translation units build in
@@ -29,6 +30,7 @@ BUILD = PKG / "build"
 OBJ = BUILD / "obj"
 LIB = BUILD / "libpaia_gemv.so"
 TORCH_LIB = BUILD / "libpaia_gemv_torch.so"
+PROBE_LIB = BUILD / "libpaia_probe.so"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
@@ -72,6 +74,14 @@ def build_lib(jobs: int | None = None) -> Path:
     return LIB
 
 
+def build_probe() -> Path:
+    """The benchmark harness's measurement kernels (streaming-read probe, empty kernel): libpaia_probe.so."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "bench_probe.hip")])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_torch_ext() -> Path:
     """Compile the torch.library ops (host C++ only) against torch's headers, linking libpaia_gemv.so."""
     import torch
@@ -96,9 +106,10 @@ def build_torch_ext() -> Path:
 def build_all() -> None:
     BUILD.mkdir(parents=True, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=2) as ex:
-        lib_f = ex.submit(build_lib)
-        lib_f.result()
+        probe_f = ex.submit(build_probe)
+        build_lib()
         build_torch_ext()
+        probe_f.result()
 
 
 def main(argv=None):

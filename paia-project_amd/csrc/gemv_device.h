@@ -79,11 +79,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// Two e4m3fn bytes (byte pair HI of word w) -> two bf16, exact for every finite code (OCP conversion on gfx950).
+// Two e4m3fn bytes (byte pair HI of word w) -> two bf16, exact for every code. v_cvt_pk_f32_fp8 (OCP e4m3 on
+// gfx950) is exact for all codes including the subnormals; an e4m3 value has at most 4 significant bits, so the
+// upper half of each f32 is that value in bf16, and one v_perm_b32 packs the two upper halves.
+// (The direct v_cvt_scalef32_pk_bf16_fp8 is not used: it does not reproduce the e4m3 subnormals.)
 template <bool HI>
 __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w)
 {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+    const auto f = __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
+    return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
 }
 
 // 8 bf16 weights (one 16-byte load) dot 8 x values.

@@ -2,7 +2,7 @@
 // Drop-in for src/paia_gemv/gemv_quant.cu:61-68 (same symbols, return codes and argument contract).
 //
 // Weights are OCP e4m3fn bytes [N][K] with one fp32 scale per row: y[n] = bf16_rn(scale[n] * sum_k e4m3(W[n,k]) x[k]).
-// The decode is the gfx950 e4m3 -> bf16 convert (exact for every finite code). Codes 0x7F/0xFF are NaN in e4m3fn and
+// The decode is the gfx950 e4m3 -> f32 convert, packed to bf16 pairs (exact for every code). Codes 0x7F/0xFF are NaN in e4m3fn and
 // decode to NaN here, as the reference's dequantiser defines them (quant_host.h:19, quant.py:16-17); the quantiser
 // never emits them.
 //

@@ -11,7 +11,7 @@
 //   * weights are streamed with raw buffer loads bounded to the row: loads past K or past N return zeros, so the hot
 //     loop has no per-lane predicates; two register buffers of R*U loads alternate so the next batch is in flight while
 //     the current one is consumed.
-//   * dequantisation happens in registers: FP8 via the gfx950 OCP e4m3->bf16 convert, INT4 by masking nibbles into
+//   * dequantisation happens in registers: FP8 via the gfx950 OCP e4m3->f32 convert packed to bf16, INT4 by masking nibbles into
 //     the mantissa of bf16 128.0; every product is a v_dot2 bf16 with fp32 accumulation.
 //   * the grid is persistent: ceil(tiles / T) blocks each take T tiles (T chosen so the grid fits the resident-block
 //     capacity of the device), which keeps the per-block x staging amortised and the load balanced.

@@ -1,0 +1,107 @@
+"""MI355X calibration: achievable streaming-read bandwidth ("B0") and the per-launch floor of graph launches.
+
+    python -m paia_bench.probe [--out PATH]
+
+  * B0 (large): one 2 GiB nontemporal streaming read, best over grid sizes and unroll depths; the reference's dev B0
+    method (src/tests/gemv_bf16_check.cu:228-252) on MI355X.
+  * B0 at the GEMV sizes: reads of S bytes from distinct slices of a 2 GiB buffer, back to back in one graph (the
+    same cold-cache rotation the GEMV timings use), so "us for S bytes" is the floor a GEMV of S bytes can reach.
+  * launch floor: back-to-back empty kernels in one graph.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent.parent
+
+
+def load_probe():
+    lib = ctypes.CDLL(str(PKG / "build" / "libpaia_probe.so"))
+    lib.paia_probe_read.restype = ctypes.c_int
+    lib.paia_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
+    lib.paia_probe_empty.restype = ctypes.c_int
+    lib.paia_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def main(argv=None):
+    import torch
+
+    from paia_gemv.loader import current_raw_stream
+    from paia_gemv.shapes import LAYER, gemv_bytes
+
+    from .timing import HBM_PEAK_GBPS, capture, replay_ms, stats
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", default=None)
+    a = ap.parse_args(argv)
+    P = load_probe()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    total = 2 * 2 ** 30
+    buf = torch.empty(total, dtype=torch.uint8, device=dev)
+    buf.random_(0, 255)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    res = {"cus": cus}
+
+    def read(ptr, nbytes, grid, unroll):
+        rc = P.paia_probe_read(ptr, nbytes, sink.data_ptr(), grid, unroll, current_raw_stream())
+        if rc:
+            raise RuntimeError(f"probe rc {rc}")
+
+    # B0 large
+    best = (0, None)
+    for mult in (2, 4, 8, 16, 32):
+        for unroll in (1, 4, 8):
+            g = capture(lambda: [read(buf.data_ptr(), total, cus * mult, unroll) for _ in range(3)], warm=1)
+            ms = stats(replay_ms(g, 5))["median"] / 3
+            gbps = total / (ms * 1e-3) / 1e9
+            print(f"[b0] grid {cus}x{mult} unroll {unroll}: {gbps:.0f} GB/s", flush=True)
+            if gbps > best[0]:
+                best = (gbps, (mult, unroll))
+            del g
+    res["b0_gbps"] = best[0]
+    res["b0_cfg"] = {"grid_per_cu": best[1][0], "unroll": best[1][1]}
+    print(f"[b0] best {best[0]:.0f} GB/s ({100 * best[0] / HBM_PEAK_GBPS:.1f}% of 8 TB/s) at {best[1]}", flush=True)
+
+    # B0 at the GEMV sizes
+    sizes = {}
+    for fmt in ("bf16", "fp8", "int4zp"):
+        for nm, N, K in LAYER["llama31_8b"] + LAYER["qwen25_7b"]:
+            sizes[f"{fmt}_{N}x{K}"] = gemv_bytes(fmt, N, K)["total"]
+    res["sized"] = {}
+    for key, S in sorted(sizes.items(), key=lambda kv: kv[1]):
+        S16 = (S + 255) // 256 * 256
+        n = max(2, total // S16)
+        R = min(2000, max(50, int(5e-3 / (S / 6e12))))
+        bestg = None
+        for mult in (4, 8, 16):
+            g = capture(lambda: [read(buf.data_ptr() + (j % n) * S16, S, cus * mult, 4) for j in range(R)], warm=1)
+            us = stats(replay_ms(g, 5))["median"] * 1e3 / R
+            del g
+            if bestg is None or us < bestg[0]:
+                bestg = (us, mult)
+        res["sized"][key] = {"bytes": S, "us": bestg[0], "gbps": S / (bestg[0] * 1e-6) / 1e9, "grid_per_cu": bestg[1]}
+        print(f"[b0 sized] {key:22s} {S / 2**20:8.2f} MiB  {bestg[0]:7.2f} us  {S / (bestg[0] * 1e-6) / 1e9:6.0f} GB/s",
+              flush=True)
+
+    # launch floor
+    for grid in (1, 256, 2048):
+        g = capture(lambda: [P.paia_probe_empty(grid, current_raw_stream()) for _ in range(1000)], warm=1)
+        us = stats(replay_ms(g, 5))["median"] * 1e3 / 1000
+        del g
+        res[f"empty_launch_us_grid{grid}"] = us
+        print(f"[launch] empty kernel grid {grid}: {us:.2f} us per launch in a graph", flush=True)
+    if a.out:
+        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.out).write_text(json.dumps(res, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

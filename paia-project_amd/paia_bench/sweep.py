@@ -1,0 +1,140 @@
+"""Variant sweep on one MI355X: time every variant of a kernel family per shape and keep the fastest.
+
+Counterpart of src/tools/dev_sweep_bf16.py:30-100 for gfx950: same idea (time each (R,U,W,S,H) tuple per N x K with
+graph timing and rotation, keep the best and the top five), same tuned-table schema keyed "NxK" under "shapes" /
+"fp8_shapes" / "int4_shapes" (paia-bench/bench/ops/ours_bf16.py:32-38, ours_quant.py:29-36).
+
+    python -m paia_bench.sweep --fmt fp8 --shapes baseline --out gpurun_out/sweep_fp8.json
+    python -m paia_bench.sweep --fmt int4zp --shapes baseline --write-tuned paia-project_amd/tuned/mi355x.json
+
+Copy 0 of each shape is checked against the CPU oracle (sampled rows) for every variant before it is timed.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+from paia_gemv.shapes import LAYER, LM_HEAD, MODELS
+
+from .cases import GemvCase, kind_of
+from .timing import HBM_PEAK_GBPS, plan_rotation, time_per_call_us
+
+TKEY = {"bf16": "shapes", "fp8": "fp8_shapes", "int4": "int4_shapes", "int4zp": "int4_shapes"}
+
+
+def shape_set(name: str, fmt: str):
+    kmult = {"bf16": 8, "fp8": 16}.get(fmt, 128)
+    out = []
+    if name in ("baseline", "all"):
+        for m in ("llama31_8b", "qwen25_7b"):
+            out += [(f"{m}:{nm}", N, K) for nm, N, K in LAYER[m]]
+        if fmt == "bf16":
+            out += [(f"{m}:lm_head", *LM_HEAD[m]) for m in ("llama31_8b", "qwen25_7b")]
+    if name in ("real", "all"):
+        for m, shp in MODELS.items():
+            out += [(f"{m}:{nm}", N, K) for nm, (N, K) in shp.items() if nm != "lm_head"]
+    seen, uniq = set(), []
+    for nm, N, K in out:
+        if K % kmult == 0 and (N, K) not in seen:
+            seen.add((N, K))
+            uniq.append((nm, N, K))
+    return uniq
+
+
+def parse_filter(expr: str):
+    import re
+    conds = []
+    for part in filter(None, (expr or "").split(",")):
+        m = re.fullmatch(r"([RUWSH])(>=|<=|=)(\d+)", part.strip())
+        if not m:
+            raise SystemExit(f"bad filter term {part!r}")
+        conds.append((m.group(1), m.group(2), int(m.group(3))))
+    ops = {"=": lambda a, b: a == b, ">=": lambda a, b: a >= b, "<=": lambda a, b: a <= b}
+    return lambda v: all(ops[o](v[k], n) for k, o, n in conds)
+
+
+def main(argv=None):
+    import torch
+
+    from oracle import oracle
+    from paia_gemv import load_lib
+
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--fmt", choices=["bf16", "fp8", "int4", "int4zp"], required=True)
+    ap.add_argument("--shapes", default="baseline", help="baseline | real | all | NxK[,NxK...]")
+    ap.add_argument("--variants", default="", help="filter, e.g. 'R=2,U>=2,H=0'")
+    ap.add_argument("--target-ms", type=float, default=2.0)
+    ap.add_argument("--samples", type=int, default=9)
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--write-tuned", default=None)
+    a = ap.parse_args(argv)
+
+    lib = load_lib()
+    dev = torch.device("cuda:0")
+    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(a.fmt, lib.variants_int4)
+    keep = parse_filter(a.variants)
+    if a.shapes in ("baseline", "real", "all"):
+        shapes = shape_set(a.shapes, a.fmt)
+    else:
+        shapes = [(s, *map(int, s.split("x"))) for s in a.shapes.split(",")]
+    results = {}
+    for nm, N, K in shapes:
+        case = GemvCase(lib, a.fmt, N, K, bias=(a.fmt != "int4" and nm.endswith("qkv") and K == 3584))
+        rot = plan_rotation(case.footprint())
+        t0 = time.time()
+        case.build(rot["n_copies"], dev)
+        rng = np.random.default_rng(0)
+        rows = np.unique(np.concatenate([np.arange(min(N, 16)), N - 1 - np.arange(min(N, 16)),
+                                         rng.integers(0, N, 64)])).astype(np.int32)
+        print(f"[sweep] {a.fmt} {nm} {N}x{K}: {rot['n_copies']} copies, built in {time.time() - t0:.1f}s", flush=True)
+        rows_res = []
+        for v in fam:
+            if not keep(v):
+                continue
+            case.variant = v["id"]
+            chk = case.check(oracle, rows=rows)
+            if not chk["ok"]:
+                print(f"  variant {v} INCORRECT {chk}", flush=True)
+                continue
+            t = time_per_call_us(case.call, rot["n_copies"], target_ms=a.target_ms, samples=a.samples,
+                                 warmup_ms=20.0)
+            gbps = case.bytes()["total"] / (t["us"] * 1e-6) / 1e9
+            rows_res.append({"variant": {k: v[k] for k in "RUWSH"}, "id": v["id"], "us": t["us"], "gbps": gbps,
+                             "cv": t.get("us_cv")})
+            print(f"  R={v['R']} U={v['U']} W={v['W']} S={v['S']} H={v['H']}: {t['us']:8.2f} us {gbps:7.0f} GB/s "
+                  f"({100 * gbps / HBM_PEAK_GBPS:4.1f}%)", flush=True)
+        rows_res.sort(key=lambda r: r["us"])
+        results[f"{N}x{K}"] = {"name": nm, "bytes": case.bytes()["total"], "ranked": rows_res}
+        if rows_res:
+            b = rows_res[0]
+            print(f"[best] {a.fmt} {nm} {N}x{K}: {b['variant']} {b['us']:.2f} us {b['gbps']:.0f} GB/s "
+                  f"({100 * b['gbps'] / HBM_PEAK_GBPS:.1f}% of 8 TB/s)", flush=True)
+        case.free()
+        torch.cuda.empty_cache()
+    if a.out:
+        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
+    if a.write_tuned:
+        f = Path(a.write_tuned)
+        tuned = json.loads(f.read_text()) if f.exists() else {"platform": "mi355x", "shapes": {}}
+        sec = tuned.setdefault(TKEY[a.fmt] if a.fmt != "int4zp" else "int4zp_shapes", {})
+        for key, r in results.items():
+            if not r["ranked"]:
+                continue
+            best = r["ranked"][0]
+            sec[key] = {"variant": best["variant"], "us": best["us"], "gbps": best["gbps"],
+                        "top5": [{"variant": x["variant"], "pct_of_best": 100 * best["us"] / x["us"]}
+                                 for x in r["ranked"][:5]],
+                        "when": time.strftime("%Y-%m-%d %H:%M")}
+        f.parent.mkdir(parents=True, exist_ok=True)
+        f.write_text(json.dumps(tuned, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
