@@ -13,6 +13,7 @@
  *
  * gfx950 limit that the reference does not have: x is staged in LDS, so K is bounded by 64 KiB of LDS per block:
  *   BF16 and FP8 K <= 32768, INT4 K <= 30720 (all Llama-3.1-8B / Qwen2.5-7B shapes fit); larger K returns -2.
+ *   Split-K variants (H=1) also keep one round of partial sums in that LDS: BF16 K <= 32256, FP8 K <= 31744.
  */
 #ifndef PAIA_GEMV_H
 #define PAIA_GEMV_H

@@ -4,6 +4,8 @@
 //   keeps the loads alive -- the MI355X counterpart of the reference's dev read probe "B0"
 //   (src/tests/gemv_bf16_check.cu:131-139,228-252). Timing it on the same byte counts as a GEMV gives the achievable
 //   bandwidth (and the fixed cost) that kernel is measured against.
+// paia_probe_copy: a plain 16-byte-per-lane copy of known size, the calibration kernel for the rocprofv3 byte counters
+//   (FETCH_SIZE should read its size once, WRITE_SIZE its size once).
 // paia_probe_empty: an empty kernel, for the per-launch floor of back-to-back launches in a graph.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -32,6 +34,14 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict
     if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads from being removed
 }
 
+__global__ void __launch_bounds__(256) copy_probe_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                         size_t n16)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 __global__ void empty_kernel() {}
 
 }  // namespace
@@ -52,6 +62,16 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     case 8: hipLaunchKernelGGL(read_probe_kernel<8>, dim3(grid), dim3(256), 0, st, p, n16, s); break;
     default: return -1;
     }
+    return (int)hipGetLastError();
+}
+
+__attribute__((visibility("default"))) int paia_probe_copy(const void* src, void* dst, size_t nbytes, int grid,
+                                                           void* stream)
+{
+    if (!src || !dst || ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) || grid <= 0)
+        return -2;
+    hipLaunchKernelGGL(copy_probe_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), nbytes / 16);
     return (int)hipGetLastError();
 }
 

@@ -117,48 +117,56 @@ __device__ __forceinline__ float dot_fp8_16B(const u32x4 w, const u32x4 x0, cons
 }
 
 // INT4: eight nibbles of one word (weights k..k+7, nibble j = weight k+j) against 8 x values staged in LDS in the
-// order (x0,x4),(x1,x5),(x2,x6),(x3,x7). Each nibble pair is turned into two bf16 (128 + q) by masking it into the
-// low mantissa bits of 0x4300 (bf16 128.0, whose ulp is 1), so sum (128+q) x = sum q x + 128 sum x; the caller
-// removes the 128 sum x term (and the zero point) with the per-segment x sums.
-__device__ __forceinline__ float i4_word_dot(uint32_t w, const u32x4 x, float acc)
+// order (x0,x2),(x4,x6),(x1,x3),(x5,x7). The even nibbles (one per byte, bits 0-3) and the odd ones (bits 4-7,
+// shifted down) are masked into two words of four bytes; one v_perm_b32 per bf16 pair then places two of those bytes
+// under a 0x43 high byte, giving bf16 (128 + q) (bf16 128.0 has an ulp of 1). So sum (128+q) x = sum q x + 128 sum x,
+// and the caller removes the 128 sum x term (and the zero point) with the per-lane x sums. 7 VALU + 4 v_dot2 per
+// 8 weights. c43 holds 0x43434343 (kept in a register: gfx9 VOP3 has no literal operand).
+__device__ __forceinline__ float i4_word_dot(uint32_t w, const u32x4 x, float acc, uint32_t c43)
 {
-    constexpr uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;
-    acc = dot2_bf16((w & kMask) | kMagic, x.x, acc);
-    acc = dot2_bf16(((w >> 4) & kMask) | kMagic, x.y, acc);
-    acc = dot2_bf16(((w >> 8) & kMask) | kMagic, x.z, acc);
-    acc = dot2_bf16(((w >> 12) & kMask) | kMagic, x.w, acc);
+    const uint32_t lo = w & 0x0F0F0F0Fu;           // bytes: q0 q2 q4 q6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;    // bytes: q1 q3 q5 q7
+    acc = dot2_bf16(__builtin_amdgcn_perm(c43, lo, 0x04010400u), x.x, acc);   // (128+q0, 128+q2)
+    acc = dot2_bf16(__builtin_amdgcn_perm(c43, lo, 0x04030402u), x.y, acc);   // (128+q4, 128+q6)
+    acc = dot2_bf16(__builtin_amdgcn_perm(c43, hi, 0x04010400u), x.z, acc);   // (128+q1, 128+q3)
+    acc = dot2_bf16(__builtin_amdgcn_perm(c43, hi, 0x04030402u), x.w, acc);   // (128+q5, 128+q7)
     return acc;
 }
 __device__ __forceinline__ float dot_i4_16B(const u32x4 w, const u32x4 x0, const u32x4 x1, const u32x4 x2,
-                                            const u32x4 x3)
+                                            const u32x4 x3, uint32_t c43)
 {
-    float d = i4_word_dot(w.x, x0, 0.0f);
-    d = i4_word_dot(w.y, x1, d);
-    d = i4_word_dot(w.z, x2, d);
-    d = i4_word_dot(w.w, x3, d);
+    float d = i4_word_dot(w.x, x0, 0.0f, c43);
+    d = i4_word_dot(w.y, x1, d, c43);
+    d = i4_word_dot(w.z, x2, d, c43);
+    d = i4_word_dot(w.w, x3, d, c43);
     return d;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// wave64 reduction: DPP within each row of 16 lanes, then the four row sums via readlane (result is wave-uniform).
-// The order of additions is fixed, so results are bitwise reproducible.
+// wave64 reduction with DPP adds: quad sums, row (16-lane) sums by rotation, then the gfx9 row broadcasts carry row 0
+// into row 1 and rows 0-1 into rows 2-3, so lane 63 ends with the wave's total. The DPP move's old value is 0 (the
+// identity of the add) for lanes outside the row mask, which lets the backend fuse each move into its v_add_f32:
+// 6 DPP adds + 1 readlane. The order of additions is fixed, so results are bitwise reproducible.
 // ---------------------------------------------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v)
+{
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = dpp_add<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);   // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);   // row_ror:8  -> every lane holds its row's sum
+    v = dpp_add<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+    v = dpp_add<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3 -> lane 63 holds the total
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v)
 {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum(float v)
-{
-    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_f32<0x124>(v);   // row_ror:4
-    v += dpp_f32<0x128>(v);   // row_ror:8
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
 }
 // Sum over the 4 lanes of a quad (result in every lane of the quad).
 __device__ __forceinline__ float quad_sum(float v)

@@ -4,19 +4,25 @@
 //
 // Replaces the reference's per-format CUDA kernels (src/paia_gemv/gemv_bf16.cuh:97-134, gemv_fp8.cuh:84-113,
 // gemv_int4.cuh:88-122) with a design for CDNA4:
-//   * wave64: a wave reads one 1 KiB "chunk" of a weight row per 16-byte buffer load (64 lanes x 16 B); R rows per
-//     wave share every x value they read.
-//   * x is staged once per block into LDS, already converted to the pairing the format's dot product wants
-//     (natural bf16 pairs for BF16/FP8; (k, k+4) pairs for INT4) plus, for INT4, the sum of each lane's 32 x values.
-//   * weights are streamed with raw buffer loads bounded to the row: loads past K or past N return zeros, so the hot
-//     loop has no per-lane predicates; two register buffers of R*U loads alternate so the next batch is in flight while
-//     the current one is consumed.
-//   * dequantisation happens in registers: FP8 via the gfx950 OCP e4m3->f32 convert packed to bf16, INT4 by masking nibbles into
-//     the mantissa of bf16 128.0; every product is a v_dot2 bf16 with fp32 accumulation.
-//   * the grid is persistent: ceil(tiles / T) blocks each take T tiles (T chosen so the grid fits the resident-block
-//     capacity of the device), which keeps the per-block x staging amortised and the load balanced.
-//   * KSPLIT (variant knob H=1): the W waves of a block share R rows and split the row's chunks round-robin; partial
-//     sums meet in LDS (fixed order, so results are reproducible). This is the split-K used for tall-K shapes.
+//   * Work unit ("item"): R consecutive rows x one K-segment of U 1-KiB chunks. A wave reads a chunk of a row with one
+//     16-byte buffer load per lane (64 lanes x 16 B = 1 KiB), so an item is R*U loads.
+//   * Each wave walks its own sequence of items and keeps the next item's R*U loads in flight while it consumes the
+//     current one (two register buffers, both filled before x is staged). There is no block-wide synchronisation in the streaming loop, so the memory
+//     pipeline never drains at row-group boundaries.
+//   * H=0: a wave owns whole row groups (all segments of a group are consecutive items of one wave; the partial sums
+//     stay in registers). Groups are dealt to the waves of the grid round-robin, so at any moment the grid streams a
+//     window of neighbouring rows.
+//     H=1 (split-K): the W waves of a block share each of the block's row groups and take its segments round-robin;
+//     per-wave partial sums go to LDS and are combined in a fixed order after a block barrier (one barrier per round
+//     of up to `round` groups, not per group). This is the split-K used for tall-K / small-N shapes.
+//   * x is staged once per block into LDS, already in the pairing each format's dot product wants (natural bf16
+//     pairs for BF16/FP8; (k, k+4) pairs for INT4) plus, for INT4, the sum of each lane's 32 x values. The first
+//     two items' weight loads are issued before the staging, so their latency overlaps it.
+//   * Weight rows are read with raw buffer loads through one descriptor per row group; a lane whose 16 bytes lie past
+//     the row end (K tails, padding segments, rows >= N) gets an out-of-range offset and reads zeros without a branch
+//     or any memory traffic.
+//   * Dequantisation happens in registers: FP8 via the gfx950 OCP e4m3 -> f32 convert packed to bf16, INT4 by
+//     masking nibbles into the mantissa of bf16 128.0; every product is a v_dot2 bf16 with fp32 accumulation.
 //
 // No MFMA: at M=1 the arithmetic intensity is ~1-4 FLOP/byte and the kernel is HBM-bound.
 #pragma once
@@ -41,8 +47,13 @@ struct GemvParams {
     uint32_t meta_bytes;    // INT4: scale bytes per row (2 G)
     uint32_t zbytes;        // INT4ZP: zero-point bytes per row (ceil(G/2))
     int nchunks;            // ceil(row_bytes / 1 KiB)
-    int tiles;              // row tiles
+    int nseg;               // ceil(nchunks / U): K-segments per row
+    int ngroups;            // ceil(N / R): row groups
+    int round;              // H=1: row groups per LDS round
 };
+
+// Out-of-range buffer offset: above any descriptor's num_records, so the load returns zeros.
+constexpr uint32_t kOOB = 0x80000000u;
 
 // LDS footprint of a launch (bytes): staged x, INT4 segment sums, split-K partials.
 template <int F>
@@ -56,44 +67,100 @@ __host__ __device__ constexpr uint32_t lds_s32_bytes(int nchunks)
     return (F == kI4 || F == kI4ZP) ? (uint32_t)nchunks * kWave * 4u : 0u;
 }
 
-// Stage x (bf16, K values) into LDS as nchunks * XQ * 64 16-byte vectors. Vector (c, j, lane) sits at index
-// (c*XQ + j)*64 + lane and holds columns c*CC + lane*CPL + 8j .. +7, where CPL = 8*XQ columns per lane and
-// CC = 64*CPL columns per chunk: a lane's x for chunk c is XQ conflict-free ds_read_b128s. Columns >= K are zero.
+// x (bf16, K values) is staged into LDS as nchunks * XQ * 64 16-byte vectors. Vector q holds x[8q .. 8q+7] (zero
+// past K) and sits at LDS index (c*XQ + j)*64 + l, where c = q / (XQ*64), l = (q mod XQ*64) / XQ, j = q mod XQ: lane
+// l's x for chunk c (columns c*CC + l*CPL .. +CPL-1, CPL = 8*XQ columns per lane, CC = 64*CPL per chunk) is XQ
+// conflict-free ds_read_b128s.
+//
+// Staging is split in two so the x loads go to memory ahead of the weight loads: x_load issues the block's first
+// XE vectors per thread (buffer loads bounded to K: zeros past K, no branch), the caller then issues its first weight
+// loads, and x_store writes them to LDS, waiting only for the x loads. Vectors beyond XE per thread (large K) are
+// loaded and stored afterwards.
+template <int XE>
+struct XRegs {
+    u32x4 v[XE];
+};
+
+template <int F, int XE>
+__device__ __forceinline__ void x_load(const GemvParams& p, XRegs<XE>& xr)
+{
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)p.K * 2u);
+#pragma unroll
+    for (int e = 0; e < XE; ++e) xr.v[e] = ld16<0>(xrs, ((uint32_t)threadIdx.x + (uint32_t)(e * blockDim.x)) * 16u, 0u);
+}
+
 template <int F>
-__device__ __forceinline__ void stage_x(const GemvParams& p, u32x4* xs, float* s32)
+__device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
+{
+    constexpr int XQ = FmtInfo<F>::kXQ;
+    const int c = q / (XQ * kWave), r = q - c * (XQ * kWave);
+    const int l = r / XQ, j = r - l * XQ;
+    if constexpr (F == kI4 || F == kI4ZP) {
+        // segment sum of this vector's 8 values (fixed order), then over the quad = the lane's 32 columns
+        float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
+                    (bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16))) +
+                   ((bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16)) +
+                    (bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16)));
+        s8 = quad_sum(s8);   // the 4 vectors of a lane-segment are 4 consecutive q in one quad of threads
+        if (j == 0) s32[c * kWave + l] = s8;
+        // pair (x0,x2),(x4,x6),(x1,x3),(x5,x7) to match the nibble order of i4_word_dot
+        const u32x4 a = v;
+        v.x = (a.x & 0xFFFFu) | (a.y << 16);
+        v.y = (a.z & 0xFFFFu) | (a.w << 16);
+        v.z = (a.x >> 16) | (a.y & 0xFFFF0000u);
+        v.w = (a.z >> 16) | (a.w & 0xFFFF0000u);
+    }
+    xs[(c * XQ + j) * kWave + l] = v;
+}
+
+// Store the XE early vectors, then load+store the rest. nq and blockDim are multiples of 4, so the `q < nq` tests are
+// uniform over each quad (quad_sum needs the whole quad).
+template <int F, int XE>
+__device__ __forceinline__ void x_store(const GemvParams& p, const XRegs<XE>& xr, u32x4* xs, float* s32)
 {
     constexpr int XQ = FmtInfo<F>::kXQ;
     const int nq = p.nchunks * XQ * kWave;
-    for (int q = (int)threadIdx.x; q < nq; q += (int)blockDim.x) {
-        const int c = q / (XQ * kWave), r = q - c * (XQ * kWave);
-        const int l = r / XQ, j = r - l * XQ;
-        const int col = q * 8;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (col < p.K) v = *reinterpret_cast<const u32x4*>(p.x + col);
-        if constexpr (F == kI4 || F == kI4ZP) {
-            // segment sum of this vector's 8 values (fixed order), then over the quad = the lane's 32 columns
-            float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
-                        (bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16))) +
-                       ((bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16)) +
-                        (bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16)));
-            s8 = quad_sum(s8);   // nq and blockDim are multiples of 4: quads are fully active together
-            if (j == 0) s32[c * kWave + l] = s8;
-            // pair (x0,x4),(x1,x5),(x2,x6),(x3,x7) to match the nibble order of i4_word_dot
-            const u32x4 a = v;
-            v.x = (a.x & 0xFFFFu) | (a.z << 16);
-            v.y = (a.x >> 16) | (a.z & 0xFFFF0000u);
-            v.z = (a.y & 0xFFFFu) | (a.w << 16);
-            v.w = (a.y >> 16) | (a.w & 0xFFFF0000u);
-        }
-        xs[(c * XQ + j) * kWave + l] = v;
+    const int T = (int)blockDim.x;
+#pragma unroll
+    for (int e = 0; e < XE; ++e) {
+        const int q = (int)threadIdx.x + e * T;
+        if (q < nq) x_put<F>(q, xr.v[e], xs, s32);
     }
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)p.K * 2u);
+    for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
 }
 
+// One item's registers: R*U weight loads, INT4 scales/zeros, the epilogue operands of lane r = row r of the group,
+// and the (wave-uniform) position of the item.
 template <int F, int R, int U>
-struct WBuf {
+struct Item {
     u32x4 w[R][U];
     uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) ? U : 1];
     uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP ? U : 1];
+    uint32_t ep_scale;   // FP8: fp32 bits of scale[row0 + lane] (lane < R)
+    uint32_t ep_bias;    // bf16 bits of bias[row0 + lane] (lane < R)
+    int group;           // row group (-1: no item)
+    int chunk0;          // first chunk of the segment
+    int slot;            // H=1: index of the group within the block's current round
+    bool last;           // last item of its group for this wave
+};
+
+// Walks a wave's items in order. H=0: groups g = first + k*gstride (k = 0..), every segment of each in turn.
+// H=1: groups of the block g = blockIdx + k*gridDim, segments s = wave, wave+W, ... of each.
+struct ItemWalker {
+    int g, s;          // next item
+    int gstride, s0, sstep, nseg, ngroups;
+    int k;             // index of the group within this block's / wave's sequence
+    __device__ __forceinline__ bool valid() const { return g < ngroups && s0 < nseg; }
+    __device__ __forceinline__ void advance()
+    {
+        s += sstep;
+        if (s >= nseg) {
+            s = s0;
+            g += gstride;
+            ++k;
+        }
+    }
 };
 
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
@@ -101,7 +168,6 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
 {
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
-    constexpr int ROWS_PER_TILE = KSPLIT ? R : R * W;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
     float* s32 = reinterpret_cast<float*>(smem + lds_x_bytes<F>(p.nchunks));
@@ -109,132 +175,238 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
 
     const int lane = lane_id();
     const int wave = wave_id();
+    const uint32_t lane16 = (uint32_t)lane * 16u;
+    // INT4 decode constant, made opaque so it stays in one register instead of a literal per instruction
+    const uint32_t c43 = (uint32_t)__builtin_amdgcn_readfirstlane(0x43434343);
+    const uint32_t row_bytes = p.row_bytes;
     const int nchunks = p.nchunks;
 
-    stage_x<F>(p, xs, s32);
-    __syncthreads();
+    ItemWalker it;
+    it.nseg = p.nseg;
+    it.ngroups = p.ngroups;
+    it.k = 0;
+    if constexpr (!KSPLIT) {
+        it.g = (int)blockIdx.x * W + wave;
+        it.gstride = (int)gridDim.x * W;
+        it.s0 = 0;
+        it.sstep = 1;
+    } else {
+        it.g = (int)blockIdx.x;
+        it.gstride = (int)gridDim.x;
+        it.s0 = wave;
+        it.sstep = W;
+    }
+    it.s = it.s0;
 
-    // chunks handled by this wave in each tile, and batches of U of them
-    const int my_chunks = KSPLIT ? (nchunks > wave ? (nchunks - wave + W - 1) / W : 0) : nchunks;
-    const int nb = (my_chunks + U - 1) / U;
-    const uint32_t voff16 = (uint32_t)lane * 16u;
-
-    int it = 0;
-    for (int tile = (int)blockIdx.x; tile < p.tiles; tile += (int)gridDim.x, ++it) {
-        const int row0 = tile * ROWS_PER_TILE + (KSPLIT ? 0 : wave * R);
-        __amdgpu_buffer_rsrc_t wr[R];
-        __amdgpu_buffer_rsrc_t mr[I4 ? R : 1];
-        __amdgpu_buffer_rsrc_t zr[F == kI4ZP ? R : 1];
+    // Per-row buffer descriptors of the current row group (wave-uniform, rebuilt only when the group changes). Each
+    // is bounded to its row: a lane whose bytes lie past the row end (K tail, padding segment) or a row >= N reads
+    // zeros with no traffic, and an INT4 lane past K also reads scale 0 (its group index is >= G), so no per-lane
+    // select is needed.
+    int bound_g = -2;
+    __amdgpu_buffer_rsrc_t rw[R];
+    __amdgpu_buffer_rsrc_t rm[I4 ? R : 1];
+    __amdgpu_buffer_rsrc_t rz[F == kI4ZP ? R : 1];
+    __amdgpu_buffer_rsrc_t rs, rb;      // epilogue: FP8 scales, bias of the group's rows (lane r = row r)
+    int nrows = 0;
+    auto bind = [&](int g) {
+        const int row0 = g < 0 ? 0 : g * R;
+        nrows = g < 0 ? 0 : min(R, p.N - row0);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = row0 + r;
-            const bool ok = row < p.N;
-            const size_t rr = ok ? (size_t)row : 0;
-            wr[r] = make_rsrc(p.W + rr * p.row_bytes, ok ? p.row_bytes : 0u);
-            if constexpr (I4) mr[r] = make_rsrc((const uint8_t*)p.meta + rr * p.meta_bytes, ok ? p.meta_bytes : 0u);
-            if constexpr (F == kI4ZP) zr[r] = make_rsrc(p.zeros + rr * p.zbytes, ok ? p.zbytes : 0u);
+            const bool ok = r < nrows;
+            const size_t row = (size_t)(row0 + r);
+            rw[r] = make_rsrc(p.W + row * row_bytes, ok ? row_bytes : 0u);
+            if constexpr (I4) rm[r] = make_rsrc((const uint8_t*)p.meta + row * p.meta_bytes, ok ? p.meta_bytes : 0u);
+            if constexpr (F == kI4ZP) rz[r] = make_rsrc(p.zeros + row * p.zbytes, ok ? p.zbytes : 0u);
         }
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        if constexpr (F == kFP8) rs = make_rsrc((const float*)p.meta + row0, (uint32_t)nrows * 4u);
+        rb = make_rsrc(p.bias ? p.bias + row0 : p.x, p.bias ? (uint32_t)nrows * 2u : 0u);
+        bound_g = g;
+    };
 
-        auto chunk_of = [&](int b, int u) { return KSPLIT ? wave + W * (b * U + u) : b * U + u; };
-
-        // Loads are issued unconditionally: a chunk past the row end reads as zeros through the bounded descriptor
-        // (no memory traffic). The whole offset goes in the per-lane voffset (soffset = 0), the operand the
-        // descriptor's range check covers. Keeping the issue branch-free lets the compiler wait for exactly the batch being
-        // consumed (s_waitcnt vmcnt(#loads of the other batch)) instead of draining both buffers.
-        auto issue = [&](WBuf<F, R, U>& B, int b) {
+    // Loads of the item `it` points at into B (size-0 descriptors when there is none: no traffic). Every load is
+    // issued unconditionally: a load under a branch would make the compiler wait for every outstanding load,
+    // including the other buffer's, before using this item.
+    auto issue = [&](Item<F, R, U>& B) {
+        const bool ok = it.valid();
+        const int g = ok ? it.g : -1;
+        if (g != bound_g) bind(g);
+        B.group = g;
+        B.chunk0 = it.s * U;
+        B.slot = KSPLIT ? it.k % p.round : 0;
+        B.last = !ok || it.s + it.sstep >= it.nseg;
+        // one VALU add per buffer; the u-th chunk is an immediate offset of the load
+        const uint32_t woff = lane16 + (uint32_t)B.chunk0 * kChunkBytes;
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t c = (uint32_t)chunk_of(b, u);
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
+        if constexpr (I4) {
+            // the lane's 32 weights of chunk c lie in group c*16 + lane/4; zero points are packed 2 groups per byte
+            const uint32_t moff = ((uint32_t)lane >> 2) * 2u + (uint32_t)B.chunk0 * 32u;
+            const uint32_t zoff = ((uint32_t)lane >> 3) + (uint32_t)B.chunk0 * 8u;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    B.w[r][u] = ld16<AUX>(wr[r], voff16 + c * kChunkBytes, 0u);
-                    if constexpr (I4) B.s[r][u] = ld_u16(mr[r], (uint32_t)(lane >> 2) * 2u + c * 32u, 0u);
-                    if constexpr (F == kI4ZP) B.z[r][u] = ld_u8(zr[r], (uint32_t)(lane >> 3) + c * 8u, 0u);
+                    B.s[r][u] = ld_u16(rm[r], moff + (uint32_t)u * 32u, 0u);
+                    if constexpr (F == kI4ZP) B.z[r][u] = ld_u8(rz[r], zoff + (uint32_t)u * 8u, 0u);
                 }
-            }
-        };
+        }
+        if constexpr (!KSPLIT) {
+            const uint32_t eoff = B.last ? (uint32_t)lane : kOOB >> 2;   // lanes >= nrows are out of range
+            if constexpr (F == kFP8) B.ep_scale = __builtin_amdgcn_raw_buffer_load_b32(rs, eoff * 4u, 0u, 0);
+            B.ep_bias = ld_u16(rb, eoff * 2u, 0u);
+        }
+        it.advance();
+    };
 
-        // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
-        // staged chunk so every product stays 0 * finite.
-        auto consume = [&](const WBuf<F, R, U>& B, int b) {
+    float acc[R];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                int c = chunk_of(b, u);
-                c = c < nchunks ? c : nchunks - 1;
-                u32x4 xv[XQ];
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
+    // staged chunk so every product stays 0 * finite.
+    auto consume = [&](const Item<F, R, U>& B) {
 #pragma unroll
-                for (int j = 0; j < XQ; ++j) xv[j] = xs[(c * XQ + j) * kWave + lane];
-                if constexpr (F == kBF16) {
+        for (int u = 0; u < U; ++u) {
+            int c = B.chunk0 + u;
+            c = c < nchunks ? c : nchunks - 1;
+            u32x4 xv[XQ];
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = dot_bf16_16B(B.w[r][u], xv[0], acc[r]);
-                } else if constexpr (F == kFP8) {
+            for (int j = 0; j < XQ; ++j) xv[j] = xs[(c * XQ + j) * kWave + lane];
+            if constexpr (F == kBF16) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
-                } else {
-                    const float sx = s32[c * kWave + lane];
+                for (int r = 0; r < R; ++r) acc[r] = dot_bf16_16B(B.w[r][u], xv[0], acc[r]);
+            } else if constexpr (F == kFP8) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3]);
-                        float s, zc;
-                        if constexpr (F == kI4) {
-                            s = f16_to_f32(B.s[r][u]);
-                            zc = 136.0f;                              // 128 (magic) + 8 (zero point)
-                        } else {
-                            s = bf16_to_f32(B.s[r][u]);
-                            const uint32_t z = (B.z[r][u] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu;
-                            zc = 128.0f + (float)z;
-                        }
-                        acc[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, d), acc[r]);
+                for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
+            } else {
+                const float sx = s32[c * kWave + lane];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
+                    float s, zc;
+                    if constexpr (F == kI4) {
+                        s = f16_to_f32(B.s[r][u]);
+                        zc = 136.0f;                              // 128 (magic) + 8 (zero point)
+                    } else {
+                        s = bf16_to_f32(B.s[r][u]);
+                        const uint32_t z = (B.z[r][u] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu;
+                        zc = 128.0f + (float)z;
                     }
+                    acc[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, d), acc[r]);
                 }
-            }
-        };
-
-        WBuf<F, R, U> A, B;
-        if (nb > 0) {
-            issue(A, 0);
-            for (int b = 0;; b += 2) {
-                issue(B, b + 1);
-                consume(A, b);
-                if (b + 1 >= nb) break;
-                issue(A, b + 2);
-                consume(B, b + 1);
-                if (b + 2 >= nb) break;
             }
         }
+    };
 
-        // reduce each row over the wave, then (split-K) over the block's waves
+    // End of a group for this wave: reduce over the wave, then store (H=0) or park the partial in LDS (H=1).
+    auto finish = [&](const Item<F, R, U>& B) {
         float tot[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) tot[r] = wave_sum(acc[r]);
-
-        auto store_row = [&](int row, float v) {
-            if (row >= p.N) return;
-            if constexpr (F == kFP8) v = v * reinterpret_cast<const float*>(p.meta)[row];
-            if (p.bias) v = v + bf16_to_f32(p.bias[row]);
-            p.y[row] = (uint16_t)f32_to_bf16_rne(v);
-        };
-
+        for (int r = 0; r < R; ++r) {
+            tot[r] = wave_sum(acc[r]);
+            acc[r] = 0.0f;
+        }
         if constexpr (!KSPLIT) {
-            if (lane == 0) {
+            // lane r stores row r of the group (one store instruction for the group)
+            float v = tot[0];
 #pragma unroll
-                for (int r = 0; r < R; ++r) store_row(row0 + r, tot[r]);
+            for (int r = 1; r < R; ++r) v = lane == r ? tot[r] : v;
+            const int row = B.group * R + lane;
+            if (lane < R && row < p.N) {
+                if constexpr (F == kFP8) v = v * __uint_as_float(B.ep_scale);
+                if (p.bias) v = v + bf16_to_f32(B.ep_bias);
+                p.y[row] = (uint16_t)f32_to_bf16_rne(v);
             }
         } else {
-            float* slot = part + (it & 1) * (W * R);
-            if (lane == 0) {
+            if (lane < R) {
+                float v = tot[0];
 #pragma unroll
-                for (int r = 0; r < R; ++r) slot[wave * R + r] = tot[r];
+                for (int r = 1; r < R; ++r) v = lane == r ? tot[r] : v;
+                part[(B.slot * W + wave) * R + lane] = v;
             }
-            __syncthreads();
-            if (wave == 0 && lane < R) {
-                float v = 0.0f;
-#pragma unroll
-                for (int w = 0; w < W; ++w) v += slot[w * R + lane];
-                store_row(row0 + lane, v);
+        }
+    };
+
+    // H=1: combine the parked partials of the groups of the round that ends with group index k_end (exclusive),
+    // in wave order, and store.
+    auto combine = [&](int k_begin, int k_end) {
+        __syncthreads();
+        const int n = (k_end - k_begin) * R;
+        const int wn = min(W, p.nseg);   // waves that own a segment (and so parked a partial) in every group
+        for (int i = (int)threadIdx.x; i < n; i += W * kWave) {
+            const int kk = i / R, r = i - kk * R;
+            const int row = ((int)blockIdx.x + (k_begin + kk) * (int)gridDim.x) * R + r;
+            const int slot = (k_begin + kk) % p.round;
+            float v = 0.0f;
+            for (int w = 0; w < wn; ++w) v += part[(slot * W + w) * R + r];
+            if (row < p.N) {
+                if constexpr (F == kFP8) v = v * reinterpret_cast<const float*>(p.meta)[row];
+                if (p.bias) v = v + bf16_to_f32(p.bias[row]);
+                p.y[row] = (uint16_t)f32_to_bf16_rne(v);
+            }
+        }
+        __syncthreads();
+    };
+
+    // Both register buffers are filled while x is staged: a wave's first two items are in flight during the staging,
+    // so a small GEMV (a few items per wave) costs one memory round trip, not one per item. From then on, the buffer
+    // just consumed is refilled with the item after the one in the other buffer.
+    // x loads first (ahead of the weights in the memory queues), then both weight buffers, then x into LDS.
+    constexpr int XE = 1024 / (W * kWave);   // early x vectors per thread: 16 KiB of x per block
+    XRegs<XE> xr;
+    x_load<F, XE>(p, xr);
+    Item<F, R, U> A, B;
+    issue(A);
+    issue(B);
+    x_store<F, XE>(p, xr, xs, s32);
+    __syncthreads();
+
+    if constexpr (!KSPLIT) {
+        if (A.group >= 0) {
+            for (;;) {
+                consume(A);
+                if (A.last) finish(A);
+                if (B.group < 0) break;
+                issue(A);
+                consume(B);
+                if (B.last) finish(B);
+                if (A.group < 0) break;
+                issue(B);
+            }
+        }
+    } else {
+        // The block's groups, in rounds of p.round; every wave walks the same groups (with its own segments), so
+        // the per-round barriers are reached by all waves. Waves without a segment (wave >= nseg) only combine.
+        const int ngb = (int)blockIdx.x < p.ngroups ? (p.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+        int k_done = 0;
+        auto step = [&](Item<F, R, U>& cur) {
+            consume(cur);
+            if (cur.last) {
+                finish(cur);
+                const int k_cur = k_done + cur.slot + 1;   // groups parked in this round so far
+                if (cur.slot == p.round - 1 || k_cur == ngb) {
+                    combine(k_done, k_cur);
+                    k_done = k_cur;
+                }
+            }
+        };
+        if (A.group >= 0) {
+            for (;;) {
+                step(A);
+                if (B.group < 0) break;
+                issue(A);
+                step(B);
+                if (A.group < 0) break;
+                issue(B);
+            }
+        } else {
+            // no segment for this wave: still take part in every round's barriers
+            for (int k0 = 0; k0 < ngb; k0 += p.round) {
+                const int k1 = min(ngb, k0 + p.round);
+                combine(k0, k1);
             }
         }
     }
@@ -253,11 +425,23 @@ DeviceFacts device_facts();
 
 // Largest LDS a launch may request (bytes). Beyond it the entry points return -2.
 constexpr uint32_t kMaxLds = 65536;
+// LDS for split-K partials (H=1): up to this much, within kMaxLds; at least one group (W*R floats) is needed.
+constexpr uint32_t kPartBytes = 8192;
 
-template <int F, int R, int U, int W, int AUX, bool KSPLIT>
-uint32_t gemv_lds_bytes(int nchunks)
+// LDS of a launch, and (H=1) the number of row groups per combine round. Returns 0 when the K is too large.
+template <int F, int R, int W, bool KSPLIT>
+uint32_t gemv_lds_plan(int nchunks, int* round)
 {
-    return lds_x_bytes<F>(nchunks) + lds_s32_bytes<F>(nchunks) + (KSPLIT ? 2u * W * R * 4u : 0u);
+    const uint32_t base = lds_x_bytes<F>(nchunks) + lds_s32_bytes<F>(nchunks);
+    *round = 1;
+    if (base > kMaxLds) return 0;
+    if (!KSPLIT) return base;
+    const uint32_t group_bytes = (uint32_t)(W * R * 4);
+    uint32_t part = kMaxLds - base < kPartBytes ? kMaxLds - base : kPartBytes;
+    part -= part % group_bytes;
+    if (part < group_bytes) return 0;
+    *round = (int)(part / group_bytes);
+    return base + part;
 }
 
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
@@ -281,10 +465,10 @@ template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 int launch_gemv(GemvParams p, hipStream_t st)
 {
     p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
-    const int rows_per_tile = KSPLIT ? R : R * W;
-    p.tiles = (p.N + rows_per_tile - 1) / rows_per_tile;
-    const uint32_t lds = gemv_lds_bytes<F, R, U, W, AUX, KSPLIT>(p.nchunks);
-    if (lds > kMaxLds) return -2;
+    p.nseg = (p.nchunks + U - 1) / U;
+    p.ngroups = (p.N + R - 1) / R;
+    const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
+    if (lds == 0) return -2;
     const DeviceFacts df = device_facts();
     int per_cu = gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>();
     if (df.lds_per_cu > 0) {
@@ -292,9 +476,12 @@ int launch_gemv(GemvParams p, hipStream_t st)
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
     }
     const int gmax = (df.cus > 0 ? df.cus : 256) * per_cu;
-    int grid = p.tiles < gmax ? p.tiles : gmax;
-    const int per_block = (p.tiles + grid - 1) / grid;
-    grid = (p.tiles + per_block - 1) / per_block;
+    // units of work dealt round-robin: row groups to waves (H=0) or to blocks (H=1)
+    const int per_block_units = KSPLIT ? 1 : W;
+    int grid = (p.ngroups + per_block_units - 1) / per_block_units;
+    if (grid > gmax) grid = gmax;
+    const int q = (p.ngroups + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
+    grid = (p.ngroups + q * per_block_units - 1) / (q * per_block_units);
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();
 }

@@ -1,0 +1,131 @@
+"""HBM bytes per launch from rocprofv3 counters, calibrated on kernels of known size.
+
+    # the workload, under the profiler (one counter pass per run: FETCH_SIZE, then WRITE_SIZE)
+    rocprofv3 --pmc FETCH_SIZE -f csv -d OUT/fetch -o run -- python3 -m paia_bench.pmc run --fmt fp8 --shape 28672x4096
+    rocprofv3 --pmc WRITE_SIZE -f csv -d OUT/write -o run -- python3 -m paia_bench.pmc run --fmt fp8 --shape 28672x4096
+    # the per-dispatch summary that bench.py reports as roofline.traffic
+    python3 -m paia_bench.pmc summarize --fetch OUT/fetch/run_counter_collection.csv \\
+        --write OUT/write/run_counter_collection.csv --out profiles/pmc_traffic.json
+
+`run` launches, eagerly and in this order: the streaming-read probe over exactly CAL_BYTES, the copy probe over
+CAL_BYTES (reads CAL_BYTES, writes CAL_BYTES), then `reps` GEMVs of the named case rotating over enough operand
+copies (>= 4 x 256 MiB) that every weight byte comes from HBM. FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in
+KiB per dispatch; `summarize` divides each by what the same counter read for the calibration kernels (bytes counted
+per byte moved), so `traffic` is in HBM bytes of the GEMV launch, next to its algorithmic bytes.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+import sys
+from pathlib import Path
+
+CAL_BYTES = 256 * 2 ** 20
+
+
+def cmd_run(a) -> int:
+    import torch
+
+    from paia_gemv import load_lib
+    from paia_gemv.loader import current_raw_stream
+
+    from .cases import GemvCase
+    from .probe import load_probe
+    from .timing import plan_rotation
+
+    dev = torch.device("cuda:0")
+    P = load_probe()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    src = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    src.random_(0, 255)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        if P.paia_probe_read(src.data_ptr(), CAL_BYTES, sink.data_ptr(), cus * 8, 1, current_raw_stream()):
+            raise RuntimeError("read probe failed")
+        if P.paia_probe_copy(src.data_ptr(), dst.data_ptr(), CAL_BYTES, cus * 8, current_raw_stream()):
+            raise RuntimeError("copy probe failed")
+    torch.cuda.synchronize()
+    del src, dst
+    lib = load_lib()
+    N, K = map(int, a.shape.split("x"))
+    case = GemvCase(lib, a.fmt, N, K, bias=a.bias, variant=a.variant)
+    n = plan_rotation(case.footprint())["n_copies"]
+    case.build(n, dev)
+    chk = case.check(rows=list(range(min(N, 64))))
+    if not chk["ok"]:
+        raise RuntimeError(f"correctness gate failed: {chk}")
+    for i in range(a.reps):
+        case.call(i % n)
+    torch.cuda.synchronize()
+    print(f"pmc run: {a.fmt} {N}x{K} variant {case.variant} x{a.reps} over {n} copies; "
+          f"algorithmic bytes {case.bytes()['total']}", flush=True)
+    return 0
+
+
+def _per_kernel(path: Path, counter: str) -> dict:
+    """{short kernel name: [per-dispatch counter value, ...]} from a rocprofv3 counter_collection CSV."""
+    out: dict = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            name = r["Kernel_Name"]
+            short = ("read_probe" if "read_probe_kernel" in name else "copy_probe" if "copy_probe_kernel" in name
+                     else name.split("(")[0].replace("void ", "") if "paia::" in name else None)
+            if short is None:
+                continue
+            out.setdefault(short, []).append(float(r["Counter_Value"]))
+    return out
+
+
+def cmd_summarize(a) -> int:
+    fetch = _per_kernel(Path(a.fetch), "FETCH_SIZE")
+    write = _per_kernel(Path(a.write), "WRITE_SIZE")
+    kib = 1024.0
+    cal_read = statistics.median(fetch["read_probe"]) * kib / CAL_BYTES          # counted bytes per byte read
+    cal_copy_r = statistics.median(fetch["copy_probe"]) * kib / CAL_BYTES
+    cal_copy_w = statistics.median(write["copy_probe"]) * kib / CAL_BYTES        # counted bytes per byte written
+    res = {"calibration": {"bytes": CAL_BYTES, "fetch_per_byte_read_probe": cal_read,
+                           "fetch_per_byte_copy_probe": cal_copy_r, "write_per_byte_copy_probe": cal_copy_w},
+           "kernels": {}}
+    for k in fetch:
+        if k.endswith("probe"):
+            continue
+        fb = statistics.median(fetch[k]) * kib / cal_read
+        wb = statistics.median(write.get(k, [0.0])) * kib / (cal_copy_w if cal_copy_w > 0 else 1.0)
+        res["kernels"][k] = {"dispatches": len(fetch[k]), "fetch_bytes": fb, "write_bytes": wb,
+                             "traffic_bytes": fb + wb}
+    if a.key:
+        only = [k for k in res["kernels"]]
+        if len(only) == 1:
+            res[a.key] = res["kernels"][only[0]] | {"kernel": only[0]}
+    Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+    Path(a.out).write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res, indent=1))
+    return 0
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    r = sub.add_parser("run")
+    r.add_argument("--fmt", default="fp8", choices=["bf16", "fp8", "int4", "int4zp"])
+    r.add_argument("--shape", default="28672x4096")
+    r.add_argument("--variant", type=int, default=None)
+    r.add_argument("--bias", action="store_true")
+    r.add_argument("--reps", type=int, default=20)
+    s = sub.add_parser("summarize")
+    s.add_argument("--fetch", required=True)
+    s.add_argument("--write", required=True)
+    s.add_argument("--out", required=True)
+    s.add_argument("--key", default=None, help="also store the (single) GEMV kernel's entry under this key")
+    a = ap.parse_args(argv)
+    return cmd_run(a) if a.cmd == "run" else cmd_summarize(a)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -24,6 +24,8 @@ def load_probe():
     lib.paia_probe_read.restype = ctypes.c_int
     lib.paia_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p]
+    lib.paia_probe_copy.restype = ctypes.c_int
+    lib.paia_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
     lib.paia_probe_empty.restype = ctypes.c_int
     lib.paia_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
     return lib

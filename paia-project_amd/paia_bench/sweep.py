@@ -7,7 +7,7 @@ graph timing and rotation, keep the best and the top five), same tuned-table sch
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --out gpurun_out/sweep_fp8.json
     python -m paia_bench.sweep --fmt int4zp --shapes baseline --write-tuned paia-project_amd/tuned/mi355x.json
 
-Copy 0 of each shape is checked against the CPU oracle (sampled rows) for every variant before it is timed.
+Copy 0 of each shape is checked against the CPU fp32 reference (sampled rows) for every variant before it is timed.
 """
 from __future__ import annotations
 
@@ -61,7 +61,6 @@ def parse_filter(expr: str):
 def main(argv=None):
     import torch
 
-    from oracle import oracle
     from paia_gemv import load_lib
 
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -97,7 +96,7 @@ def main(argv=None):
             if not keep(v):
                 continue
             case.variant = v["id"]
-            chk = case.check(oracle, rows=rows)
+            chk = case.check(rows=rows)
             if not chk["ok"]:
                 print(f"  variant {v} INCORRECT {chk}", flush=True)
                 continue
