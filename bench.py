@@ -1,18 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the paia_gemv hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH] [--no-cpu] [--no-chain]
 
 Workload (the metric's configuration): FP8 W8A16 M=1 GEMVs at the Llama-3.1-8B per-layer shapes
 qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336, OCP e4m3fn weights with a per-row fp32 scale, bf16
 activations and outputs. One step = the four GEMVs of one decoder layer; steps rotate over L distinct layer copies
 whose total (>= 4 x 256 MiB) defeats the Infinity Cache, so every weight byte comes from HBM. The timed region is one
-hipGraph replay of K steps, bracketed by device synchronisation, with all inputs resident in HBM.
+hipGraph replay of K steps, bracketed by device synchronisation, with all inputs resident in HBM. Each GEMV uses the
+library's per-shape variant (paia_gemv_pick_variant, the frozen MI355X sweep in paia-project_amd/tuned/mi355x.json).
 
 Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmic GB/s of the step, plus
   per_gemv      us/GEMV, GB/s and % of 8 TB/s for each shape (graph of R back-to-back launches, rotating copies)
-  roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time, vs 8 TB/s
-  cpu_baseline  the reference's CPU path (dequantise, then fp32 matmul) on the host cores, on a bounded sample
+  roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time (hipEvents on the launch
+                stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the committed rocprofv3
+                FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels of known size
+  chain         BASELINE configs[4]: 32 layers x 4 GEMVs + bf16 lm_head as one hipGraph, INT4 (asymmetric g128) and
+                FP8: us per token-step and aggregate GB/s (skipped with --no-chain)
+  cpu_baseline  the CPU path (oracle dequantisation + torch fp32 matmul) on the host cores, on a bounded sample
 Copy 0 of every operand set is checked against the CPU fp32 reference (torch dequantisation + matmul, the reference
 harness's gate) before anything is timed. The CPU oracle is used only by the cpu_baseline leg, as the CPU path timed.
 """
@@ -39,9 +44,11 @@ def log(msg):
 
 
 def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
-    """The reference's CPU path: dequantise with the oracle (C, one thread), then an fp32 torch
-    matmul on the host cores. Runs over the layer's four shapes (seeded copy-0 operands) until ~budget_s."""
-    import numpy as np
+    """The reference's CPU path (dequantise, then an fp32 matmul): the oracle's C dequantiser
+    (one thread) and torch's CPU fp32 matmul on the host cores, over the layer's four shapes (seeded copy-0 operands)
+    until ~budget_s."""
+    import platform
+
     import torch
     from paia_bench.inputs import as_numpy
 
@@ -69,7 +76,6 @@ def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
         if time.perf_counter() - t_start > budget_s or steps >= 20:
             break
     total = t_deq + t_mm
-    import platform
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -78,24 +84,37 @@ def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
                 break
     except OSError:
         model = platform.processor()
-    return {"value": nbytes / total / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(nbytes / total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{steps} layer step(s) x 4 FP8 GEMVs (Llama-3.1-8B qkv/o/gate_up/down, seeded copy 0): "
-                      f"oracle dequant (1 thread) + torch fp32 matmul ({threads} threads); "
+                      f"oracle C dequant (1 thread) + torch fp32 matmul ({threads} threads); "
                       f"us per layer step {total / steps * 1e6:.0f} (dequant {t_deq / steps * 1e6:.0f}, "
                       f"matmul {t_mm / steps * 1e6:.0f}); cpu {model}",
-            "matmul_only_gbps": nbytes / t_mm / 1e9 if t_mm > 0 else None}
+            "us_per_layer_step": round(total / steps * 1e6, 1),
+            "matmul_only_gbps": round(nbytes / t_mm / 1e9, 3) if t_mm > 0 else None}
 
 
-def load_traffic(kernel_key: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary (profiles/), or None."""
+def load_traffic(case_name: str):
+    """HBM bytes per launch of this GEMV case from the committed rocprofv3 PMC summary (profiles/pmc_traffic.json,
+    written by `python -m paia_bench.pmc summarize`), or None if that case was not profiled."""
     f = ROOT / "profiles" / "pmc_traffic.json"
     if not f.exists():
         return None
     try:
         d = json.loads(f.read_text())
-        return d.get(kernel_key, {}).get("traffic_bytes")
-    except (OSError, ValueError):
+        e = d.get("cases", {}).get(case_name)
+        return None if e is None else {"bytes": round(e["traffic_bytes"]), "kernel": e.get("kernel"),
+                                       "fetch_bytes": round(e["fetch_bytes"]), "write_bytes": round(e["write_bytes"])}
+    except (OSError, ValueError, KeyError):
         return None
+
+
+def kernel_name(lib, case) -> str:
+    """The template instance of gemv_kernel a case launches (as rocprofv3 names it)."""
+    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(case.fmt, lib.variants_int4)
+    v = fam[case.variant]
+    F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[case.fmt]
+    aux = (2 if v["S"] else 0) if case.fmt == "bf16" else 2
+    return f"paia::gemv_kernel<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
 
 
 def main(argv=None):
@@ -105,11 +124,12 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--report", type=str, default=None, help="also write a detailed JSON report here")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-chain", action="store_true", help="skip the decode-chain (configs[4]) measurement")
     a = ap.parse_args(argv)
     if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the M=1 GEMV shards along N "
-              "with no collective, so N-GPU throughput is N x the one-GPU figure on N/N-row shards. Run --gpus 1.",
-              file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}). The M=1 GEMV shards along N "
+              "with no collective (each GPU streams its N/g rows with the full x), so the one-GPU figure on one "
+              "GPU's share is what this benchmark reports. Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
@@ -149,6 +169,8 @@ def main(argv=None):
                     c.call(s % L)
         return run
 
+    # warmup replays, then the timed replay of exactly K steps, bracketed by device synchronisation; the events are
+    # recorded on the stream the GEMVs launch on (torch's current stream, which the ctypes calls use)
     g_warm = capture(steps_fn(max(1, a.warmup)), warm=1)
     g_timed = capture(steps_fn(a.steps), warm=0)
     g_warm.replay()
@@ -173,33 +195,50 @@ def main(argv=None):
         t = time_per_call_us(c.call, L)
         gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
         per[c.name] = {"us": round(t["us"], 3), "gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1),
-                       "variant": lib.variants_fp8[c.variant], "bytes": c.bytes()["total"], "R": t["R"]}
+                       "variant": lib.variants_fp8[c.variant], "kernel": kernel_name(lib, c),
+                       "bytes": c.bytes()["total"], "R": t["R"]}
         log(f"  {c.name}: {t['us']:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s)")
 
     dom = max(cases, key=lambda c: c.bytes()["total"])
     dom_us = per[dom.name]["us"]
     achieved = dom.bytes()["total"] / (dom_us * 1e-6) / 1e9
+    traffic = load_traffic(dom.name)
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBPS, 4), "traffic": load_traffic(dom.name),
-            "kernel": dom.name, "avg_launch_us": dom_us, "algorithmic_bytes": dom.bytes()["total"]}
+            "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic["bytes"] if traffic else None,
+            "kernel": kernel_name(lib, dom), "case": dom.name, "avg_launch_us": dom_us,
+            "algorithmic_bytes": dom.bytes()["total"],
+            "traffic_detail": traffic}
+    for c in cases:
+        c.free()
+    torch.cuda.empty_cache()
+
+    chain = None
+    if not a.no_chain:
+        from paia_bench.chain import run_chain
+        log("decode chain (configs[4]) ...")
+        chain = {f: run_chain(lib, f, log=log) for f in ("int4zp", "fp8")}
 
     cpu = None
     if not a.no_cpu:
-        log("cpu baseline ...")
         from oracle import oracle
-        cpu = cpu_baseline(oracle, cases)
+        log("cpu baseline ...")
+        from paia_bench.inputs import make_operands
+        cpu_cases = [GemvCase(lib, "fp8", N, K, name=f"fp8_{nm}_{N}x{K}") for nm, N, K in shapes]
+        for c in cpu_cases:
+            c.ops0 = make_operands("fp8", c.N, c.K)
+        cpu = cpu_baseline(oracle, cpu_cases)
         log(f"  cpu {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "fp8_e4m3 weights x bf16 activations, fp32 accumulate",
+           "vs_baseline": None, "dtype": "fp8e4m3 weights x bf16 activations, fp32 accumulate",
            "data": "synthetic (seeded N(0,0.02) weights quantised to e4m3fn; N(0,1) bf16 x)",
            "config": {"workload": "FP8 W8A16 GEMV, M=1, Llama-3.1-8B layer: qkv 6144x4096, o 4096x4096, "
                                   "gate_up 28672x4096, down 4096x14336 (BASELINE configs[1])",
                       "layer_copies": L, "rotation_bytes": L * layer_bytes, "step_bytes": step_bytes,
                       "us_per_layer_step": round(ms_per_step * 1e3, 3),
                       "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1)},
-           "per_gemv": per, "roofline": roof, "cpu_baseline": cpu}
+           "per_gemv": per, "roofline": roof, "chain": chain, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
     if a.report:
         Path(a.report).parent.mkdir(parents=True, exist_ok=True)

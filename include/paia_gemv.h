@@ -82,8 +82,8 @@ PAIA_API int paia_dequant_int4_zp(const void* Wq, const void* scales, const void
                                   void* stream);
 
 /* no reference counterpart (the reference picks variants in Python from src/tuned/<platform>.json,
- * paia-bench/bench/ops/ours_bf16.py:32-38): the library's per-shape variant for kind 0 BF16, 1 FP8, 2 INT4 (both
- * INT4 formats). Always returns a valid index of that kind's table. */
+ * paia-bench/bench/ops/ours_bf16.py:32-38): the library's per-shape variant for kind 0 BF16, 1 FP8, 2 INT4 reference
+ * format, 3 INT4 asymmetric (an index of the paia_gemv_int4 table). Always returns a valid index of that table. */
 PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
 
 /* no reference counterpart: a human-readable build tag */

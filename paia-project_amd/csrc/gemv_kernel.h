@@ -6,8 +6,8 @@
 // gemv_int4.cuh:88-122) with a design for CDNA4:
 //   * Work unit ("item"): R consecutive rows x one K-segment of U 1-KiB chunks. A wave reads a chunk of a row with one
 //     16-byte buffer load per lane (64 lanes x 16 B = 1 KiB), so an item is R*U loads.
-//   * Each wave walks its own sequence of items and keeps the next item's R*U loads in flight while it consumes the
-//     current one (two register buffers, both filled before x is staged). There is no block-wide synchronisation in the streaming loop, so the memory
+//   * Each wave walks its own sequence of items and keeps the next item's loads in flight while it consumes the
+//     current one (two register buffers, both filled while x is staged). There is no block-wide synchronisation in the streaming loop, so the memory
 //     pipeline never drains at row-group boundaries.
 //   * H=0: a wave owns whole row groups (all segments of a group are consecutive items of one wave; the partial sums
 //     stay in registers). Groups are dealt to the waves of the grid round-robin, so at any moment the grid streams a
@@ -130,24 +130,31 @@ __device__ __forceinline__ void x_store(const GemvParams& p, const XRegs<XE>& xr
     for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
 }
 
-// One item's registers: R*U weight loads, INT4 scales/zeros, the epilogue operands of lane r = row r of the group,
-// and the (wave-uniform) position of the item.
+// One item's registers: R*U weight loads, INT4 scales/zeros, and the (wave-uniform) position of the item.
 template <int F, int R, int U>
 struct Item {
     u32x4 w[R][U];
     uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) ? U : 1];
     uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP ? U : 1];
-    uint32_t ep_scale;   // FP8: fp32 bits of scale[row0 + lane] (lane < R)
-    uint32_t ep_bias;    // bf16 bits of bias[row0 + lane] (lane < R)
     int group;           // row group (-1: no item)
     int chunk0;          // first chunk of the segment
-    int slot;            // H=1: index of the group within the block's current round
+    int k;               // index of the group in this wave's (H=0) or block's (H=1) sequence
     bool last;           // last item of its group for this wave
 };
+
+// Item buffers in flight per wave. Two: measured on MI355X, deeper pipelines of small items (8 x 1 KiB, 4 x 2 KiB)
+// were slower than two buffers of larger items (2 x 4 KiB) at the same bytes in flight, because every item pays
+// its issue/offset/epilogue bookkeeping; the bytes in flight are set by the item size R*U instead.
+template <int R, int U>
+__host__ __device__ constexpr int pipe_depth()
+{
+    return 2;
+}
 
 // Walks a wave's items in order. H=0: groups g = first + k*gstride (k = 0..), every segment of each in turn.
 // H=1: groups of the block g = blockIdx + k*gridDim, segments s = wave, wave+W, ... of each.
 struct ItemWalker {
+    int g0;            // first group of the sequence
     int g, s;          // next item
     int gstride, s0, sstep, nseg, ngroups;
     int k;             // index of the group within this block's / wave's sequence
@@ -197,6 +204,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         it.sstep = W;
     }
     it.s = it.s0;
+    it.g0 = it.g;
 
     // Per-row buffer descriptors of the current row group (wave-uniform, rebuilt only when the group changes). Each
     // is bounded to its row: a lane whose bytes lie past the row end (K tail, padding segment) or a row >= N reads
@@ -206,7 +214,6 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     __amdgpu_buffer_rsrc_t rw[R];
     __amdgpu_buffer_rsrc_t rm[I4 ? R : 1];
     __amdgpu_buffer_rsrc_t rz[F == kI4ZP ? R : 1];
-    __amdgpu_buffer_rsrc_t rs, rb;      // epilogue: FP8 scales, bias of the group's rows (lane r = row r)
     int nrows = 0;
     auto bind = [&](int g) {
         const int row0 = g < 0 ? 0 : g * R;
@@ -219,9 +226,21 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
             if constexpr (I4) rm[r] = make_rsrc((const uint8_t*)p.meta + row * p.meta_bytes, ok ? p.meta_bytes : 0u);
             if constexpr (F == kI4ZP) rz[r] = make_rsrc(p.zeros + row * p.zbytes, ok ? p.zbytes : 0u);
         }
-        if constexpr (F == kFP8) rs = make_rsrc((const float*)p.meta + row0, (uint32_t)nrows * 4u);
-        rb = make_rsrc(p.bias ? p.bias + row0 : p.x, p.bias ? (uint32_t)nrows * 2u : 0u);
         bound_g = g;
+    };
+
+    // H=0 epilogue operands, loaded once per wave (per window of ep_groups groups): lane kk*R + r holds FP8 scale and
+    // bias of row r of the wave's group number (window*ep_groups + kk). Rows past N or past the wave's groups read 0.
+    constexpr int ep_groups = kWave / R;
+    uint32_t ep_scale = 0u, ep_bias = 0u;
+    auto ep_load = [&](int k_first) {
+        const int kk = lane / R, r = lane - kk * R;
+        const int g = it.g0 + (k_first + kk) * it.gstride;
+        const bool ok = kk < ep_groups && g < p.ngroups && g * R + r < p.N;
+        const uint32_t row = ok ? (uint32_t)(g * R + r) : kOOB >> 2;
+        if constexpr (F == kFP8)
+            ep_scale = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p.meta, (uint32_t)p.N * 4u), row * 4u, 0u, 0);
+        ep_bias = ld_u16(make_rsrc(p.bias ? p.bias : p.x, p.bias ? (uint32_t)p.N * 2u : 0u), row * 2u, 0u);
     };
 
     // Loads of the item `it` points at into B (size-0 descriptors when there is none: no traffic). Every load is
@@ -233,7 +252,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         if (g != bound_g) bind(g);
         B.group = g;
         B.chunk0 = it.s * U;
-        B.slot = KSPLIT ? it.k % p.round : 0;
+        B.k = it.k;
         B.last = !ok || it.s + it.sstep >= it.nseg;
         // one VALU add per buffer; the u-th chunk is an immediate offset of the load
         const uint32_t woff = lane16 + (uint32_t)B.chunk0 * kChunkBytes;
@@ -252,11 +271,6 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
                     B.s[r][u] = ld_u16(rm[r], moff + (uint32_t)u * 32u, 0u);
                     if constexpr (F == kI4ZP) B.z[r][u] = ld_u8(rz[r], zoff + (uint32_t)u * 8u, 0u);
                 }
-        }
-        if constexpr (!KSPLIT) {
-            const uint32_t eoff = B.last ? (uint32_t)lane : kOOB >> 2;   // lanes >= nrows are out of range
-            if constexpr (F == kFP8) B.ep_scale = __builtin_amdgcn_raw_buffer_load_b32(rs, eoff * 4u, 0u, 0);
-            B.ep_bias = ld_u16(rb, eoff * 2u, 0u);
         }
         it.advance();
     };
@@ -310,14 +324,18 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
             acc[r] = 0.0f;
         }
         if constexpr (!KSPLIT) {
-            // lane r stores row r of the group (one store instruction for the group)
+            // lanes kk*R .. kk*R+R-1 hold this group's epilogue operands (kk = the group's slot in the window) and
+            // store its R rows: one store instruction per group
+            const int kk = B.k % ep_groups;
+            if (kk == 0 && B.k > 0) ep_load(B.k);   // next window (only for waves with more than 64/R groups)
+            const int r = lane - kk * R;
             float v = tot[0];
 #pragma unroll
-            for (int r = 1; r < R; ++r) v = lane == r ? tot[r] : v;
-            const int row = B.group * R + lane;
-            if (lane < R && row < p.N) {
-                if constexpr (F == kFP8) v = v * __uint_as_float(B.ep_scale);
-                if (p.bias) v = v + bf16_to_f32(B.ep_bias);
+            for (int i = 1; i < R; ++i) v = r == i ? tot[i] : v;
+            const int row = B.group * R + r;
+            if (r >= 0 && r < R && row < p.N) {
+                if constexpr (F == kFP8) v = v * __uint_as_float(ep_scale);
+                if (p.bias) v = v + bf16_to_f32(ep_bias);
                 p.y[row] = (uint16_t)f32_to_bf16_rne(v);
             }
         } else {
@@ -325,7 +343,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
                 float v = tot[0];
 #pragma unroll
                 for (int r = 1; r < R; ++r) v = lane == r ? tot[r] : v;
-                part[(B.slot * W + wave) * R + lane] = v;
+                part[((B.k % p.round) * W + wave) * R + lane] = v;
             }
         }
     };
@@ -351,30 +369,32 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         __syncthreads();
     };
 
-    // Both register buffers are filled while x is staged: a wave's first two items are in flight during the staging,
-    // so a small GEMV (a few items per wave) costs one memory round trip, not one per item. From then on, the buffer
-    // just consumed is refilled with the item after the one in the other buffer.
-    // x loads first (ahead of the weights in the memory queues), then both weight buffers, then x into LDS.
+    // x loads first (ahead of the weight loads in the memory queues), then all D item buffers, then x into LDS.
+    // All D buffers are in flight while x is staged, so a small GEMV (a few items per wave) costs one memory round
+    // trip. From then on, the buffer just consumed is refilled with the item D places further on (D = 2).
     constexpr int XE = 1024 / (W * kWave);   // early x vectors per thread: 16 KiB of x per block
+    constexpr int D = pipe_depth<R, U>();
     XRegs<XE> xr;
     x_load<F, XE>(p, xr);
-    Item<F, R, U> A, B;
-    issue(A);
-    issue(B);
+    if constexpr (!KSPLIT) ep_load(0);
+    Item<F, R, U> buf[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(buf[d]);
     x_store<F, XE>(p, xr, xs, s32);
     __syncthreads();
 
     if constexpr (!KSPLIT) {
-        if (A.group >= 0) {
-            for (;;) {
-                consume(A);
-                if (A.last) finish(A);
-                if (B.group < 0) break;
-                issue(A);
-                consume(B);
-                if (B.last) finish(B);
-                if (A.group < 0) break;
-                issue(B);
+        bool done = buf[0].group < 0;
+        while (!done) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                if (buf[d].group < 0) {
+                    done = true;
+                    break;
+                }
+                consume(buf[d]);
+                if (buf[d].last) finish(buf[d]);
+                issue(buf[d]);
             }
         }
     } else {
@@ -382,25 +402,26 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         // the per-round barriers are reached by all waves. Waves without a segment (wave >= nseg) only combine.
         const int ngb = (int)blockIdx.x < p.ngroups ? (p.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
         int k_done = 0;
-        auto step = [&](Item<F, R, U>& cur) {
-            consume(cur);
-            if (cur.last) {
-                finish(cur);
-                const int k_cur = k_done + cur.slot + 1;   // groups parked in this round so far
-                if (cur.slot == p.round - 1 || k_cur == ngb) {
-                    combine(k_done, k_cur);
-                    k_done = k_cur;
+        if (buf[0].group >= 0) {
+            bool done = false;
+            while (!done) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    if (buf[d].group < 0) {
+                        done = true;
+                        break;
+                    }
+                    consume(buf[d]);
+                    if (buf[d].last) {
+                        finish(buf[d]);
+                        const int k_cur = buf[d].k + 1;   // groups parked so far
+                        if (k_cur - k_done == p.round || k_cur == ngb) {
+                            combine(k_done, k_cur);
+                            k_done = k_cur;
+                        }
+                    }
+                    issue(buf[d]);
                 }
-            }
-        };
-        if (A.group >= 0) {
-            for (;;) {
-                step(A);
-                if (B.group < 0) break;
-                issue(A);
-                step(B);
-                if (A.group < 0) break;
-                issue(B);
             }
         } else {
             // no segment for this wave: still take part in every round's barriers
@@ -422,6 +443,12 @@ struct DeviceFacts {
     int lds_per_cu = 0;
 };
 DeviceFacts device_facts();
+
+// Resident waves per CU the persistent grid aims for (each block stages x, so more blocks mean more x traffic).
+#ifndef PAIA_GEMV_MAX_WAVES_PER_CU
+#define PAIA_GEMV_MAX_WAVES_PER_CU 32
+#endif
+constexpr int kMaxWavesPerCu = PAIA_GEMV_MAX_WAVES_PER_CU;
 
 // Largest LDS a launch may request (bytes). Beyond it the entry points return -2.
 constexpr uint32_t kMaxLds = 65536;
@@ -475,6 +502,7 @@ int launch_gemv(GemvParams p, hipStream_t st)
         const int by_lds = (int)(df.lds_per_cu / (lds ? lds : 1u));
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
     }
+    if (per_cu * W > kMaxWavesPerCu) per_cu = kMaxWavesPerCu / W > 0 ? kMaxWavesPerCu / W : 1;
     const int gmax = (df.cus > 0 ? df.cus : 256) * per_cu;
     // units of work dealt round-robin: row groups to waves (H=0) or to blocks (H=1)
     const int per_block_units = KSPLIT ? 1 : W;

@@ -19,7 +19,7 @@
 
 namespace {
 
-enum Kind { kBF16 = 0, kFP8 = 1, kINT4 = 2 };
+enum Kind { kBF16 = 0, kFP8 = 1, kINT4 = 2, kINT4ZP = 3 };
 
 void check_rc(int rc, const char* what)
 {
@@ -148,7 +148,7 @@ void gemv_int4_zp_out(const at::Tensor& Wq, const at::Tensor& scales, const at::
     check_out(out, x, N);
     c10::DeviceGuard g(Wq.device());
     check_rc(paia_gemv_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), x.data_ptr(), opt_ptr(bias, N),
-                               out.data_ptr(), (int)N, (int)K, pick(variant, kINT4, N, K), stream_of(Wq)),
+                               out.data_ptr(), (int)N, (int)K, pick(variant, kINT4ZP, N, K), stream_of(Wq)),
              "paia_gemv_int4_zp");
 }
 at::Tensor gemv_int4_zp(const at::Tensor& Wq, const at::Tensor& scales, const at::Tensor& zeros, const at::Tensor& x,

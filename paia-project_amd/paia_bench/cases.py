@@ -1,9 +1,9 @@
 """One GEMV configuration on the device: n_copies operand sets for cache-defeating rotation and a launch closure.
 
 Copy 0 holds the seeded BASELINE operands (paia_bench.inputs), the one checked for correctness before any timing
-(as paia-bench/bench/run.py:236-240 gates cells). Copies 1.. hold random codes of the same format generated on the
-device: the kernels have no data-dependent control flow, so timing does not depend on the values
-(paia-bench/bench/ops/ours_quant.py:3-6 uses the same convention).
+(as paia-bench/bench/run.py:236-240 gates cells). Copies 1.. are drawn on the device with the same distributions
+(the reference fills them with random codes, paia-bench/bench/ops/ours_quant.py:3-6; the kernels have no
+data-dependent control flow, so timing does not depend on the values either way).
 """
 from __future__ import annotations
 
@@ -26,7 +26,7 @@ class GemvCase:
                  mode: str = "fused", name: str | None = None):
         self.lib, self.fmt, self.N, self.K, self.bias, self.mode = lib, fmt, N, K, bias, mode
         self.name = name or f"{fmt}_{N}x{K}"
-        self.variant = lib.pick_variant(kind_of(fmt), N, K) if variant is None else int(variant)
+        self.variant = lib.pick_variant(fmt, N, K) if variant is None else int(variant)
         self.copies: list = []
         self.ptrs: list = []
         self.scratch = None
@@ -41,21 +41,20 @@ class GemvCase:
 
     # ---- operands ----------------------------------------------------------------------------------------
     def _random_copy(self, dev, g):
+        """Another operand set with the BASELINE distributions (paia_bench.inputs), drawn on the device."""
         N, K, G = self.N, self.K, self.K // 128
-        c = {"N": N, "K": K, "x": torch.randn(K, device=dev, generator=g).to(torch.bfloat16)}
-        u8 = lambda *s: torch.randint(0, 256, s, device=dev, generator=g, dtype=torch.uint8)
+        c = {"N": N, "K": K}
         if self.fmt == "bf16":
             c["W"] = (0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16)
         elif self.fmt == "fp8":
-            c["Wq"] = u8(N, K)
-            c["scale"] = torch.rand(N, device=dev, generator=g).mul_(0.01).add_(1e-3)
+            c["Wq"], c["scale"] = quant.quantize_fp8_rowwise(0.02 * torch.randn(N, K, device=dev, generator=g))
         elif self.fmt == "int4":
-            c["Wq"] = u8(N, K // 2)
-            c["scales"] = torch.rand(N, G, device=dev, generator=g).mul_(0.01).add_(1e-3).half()
+            c["Wq"], c["scales"] = quant.quantize_int4_g128(0.02 * torch.randn(N, K, device=dev, generator=g))
         else:
-            c["Wq"] = u8(N, K // 2)
-            c["scales"] = torch.rand(N, G, device=dev, generator=g).mul_(0.01).add_(1e-3).bfloat16()
-            c["zeros"] = u8(N, (G + 1) // 2)
+            c["Wq"] = torch.randint(0, 256, (N, K // 2), device=dev, generator=g, dtype=torch.uint8)
+            c["scales"] = (0.001 + 0.009 * torch.rand(N, G, device=dev, generator=g)).to(torch.bfloat16)
+            c["zeros"] = quant.pack_zeros(torch.randint(0, 16, (N, G), device=dev, generator=g, dtype=torch.uint8))
+        c["x"] = torch.randn(K, device=dev, generator=g).to(torch.bfloat16)
         c["bias"] = (0.02 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16) if self.bias else None
         return c
 

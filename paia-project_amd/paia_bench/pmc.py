@@ -5,7 +5,8 @@
     rocprofv3 --pmc WRITE_SIZE -f csv -d OUT/write -o run -- python3 -m paia_bench.pmc run --fmt fp8 --shape 28672x4096
     # the per-dispatch summary that bench.py reports as roofline.traffic
     python3 -m paia_bench.pmc summarize --fetch OUT/fetch/run_counter_collection.csv \\
-        --write OUT/write/run_counter_collection.csv --out profiles/pmc_traffic.json
+        --write OUT/write/run_counter_collection.csv --out profiles/pmc_traffic.json \\
+        --case fp8_gate_up_28672x4096 --fmt fp8 --shape 28672x4096
 
 `run` launches, eagerly and in this order: the streaming-read probe over exactly CAL_BYTES, the copy probe over
 CAL_BYTES (reads CAL_BYTES, writes CAL_BYTES), then `reps` GEMVs of the named case rotating over enough operand
@@ -83,29 +84,34 @@ def _per_kernel(path: Path, counter: str) -> dict:
 
 
 def cmd_summarize(a) -> int:
+    """Merge one profiled case into the summary file: {"calibration": ..., "cases": {name: {...}}}."""
+    from paia_gemv.shapes import gemv_bytes
+
     fetch = _per_kernel(Path(a.fetch), "FETCH_SIZE")
     write = _per_kernel(Path(a.write), "WRITE_SIZE")
     kib = 1024.0
     cal_read = statistics.median(fetch["read_probe"]) * kib / CAL_BYTES          # counted bytes per byte read
     cal_copy_r = statistics.median(fetch["copy_probe"]) * kib / CAL_BYTES
     cal_copy_w = statistics.median(write["copy_probe"]) * kib / CAL_BYTES        # counted bytes per byte written
-    res = {"calibration": {"bytes": CAL_BYTES, "fetch_per_byte_read_probe": cal_read,
-                           "fetch_per_byte_copy_probe": cal_copy_r, "write_per_byte_copy_probe": cal_copy_w},
-           "kernels": {}}
-    for k in fetch:
-        if k.endswith("probe"):
-            continue
-        fb = statistics.median(fetch[k]) * kib / cal_read
-        wb = statistics.median(write.get(k, [0.0])) * kib / (cal_copy_w if cal_copy_w > 0 else 1.0)
-        res["kernels"][k] = {"dispatches": len(fetch[k]), "fetch_bytes": fb, "write_bytes": wb,
-                             "traffic_bytes": fb + wb}
-    if a.key:
-        only = [k for k in res["kernels"]]
-        if len(only) == 1:
-            res[a.key] = res["kernels"][only[0]] | {"kernel": only[0]}
-    Path(a.out).parent.mkdir(parents=True, exist_ok=True)
-    Path(a.out).write_text(json.dumps(res, indent=1) + "\n")
-    print(json.dumps(res, indent=1))
+    gemv = [k for k in fetch if not k.endswith("probe")]
+    if len(gemv) != 1:
+        raise SystemExit(f"expected one GEMV kernel in the trace, found {gemv}")
+    k = gemv[0]
+    N, K = map(int, a.shape.split("x"))
+    fb = statistics.median(fetch[k]) * kib / cal_read
+    wb = statistics.median(write.get(k, [0.0])) * kib / cal_copy_w
+    out = Path(a.out)
+    res = json.loads(out.read_text()) if out.exists() else {}
+    res["calibration"] = {"bytes": CAL_BYTES, "fetch_per_byte_read_probe": round(cal_read, 4),
+                          "fetch_per_byte_copy_probe": round(cal_copy_r, 4),
+                          "write_per_byte_copy_probe": round(cal_copy_w, 4)}
+    alg = gemv_bytes(a.fmt, N, K, a.bias)["total"]
+    res.setdefault("cases", {})[a.case] = {
+        "kernel": k, "dispatches": len(fetch[k]), "fetch_bytes": round(fb), "write_bytes": round(wb),
+        "traffic_bytes": round(fb + wb), "algorithmic_bytes": alg, "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res["cases"][a.case] | {"calibration": res["calibration"]}, indent=1))
     return 0
 
 
@@ -122,7 +128,10 @@ def main(argv=None) -> int:
     s.add_argument("--fetch", required=True)
     s.add_argument("--write", required=True)
     s.add_argument("--out", required=True)
-    s.add_argument("--key", default=None, help="also store the (single) GEMV kernel's entry under this key")
+    s.add_argument("--case", required=True, help="name the entry is stored under (bench.py's case name)")
+    s.add_argument("--fmt", default="fp8", choices=["bf16", "fp8", "int4", "int4zp"])
+    s.add_argument("--shape", default="28672x4096")
+    s.add_argument("--bias", action="store_true")
     a = ap.parse_args(argv)
     return cmd_run(a) if a.cmd == "run" else cmd_summarize(a)
 

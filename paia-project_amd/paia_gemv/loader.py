@@ -155,8 +155,8 @@ class GemvLib:
                     "paia_dequant_int4_zp")
 
     def pick_variant(self, kind, N, K):
-        """Library's per-shape variant: kind 'bf16' | 'fp8' | 'int4' (both INT4 formats)."""
-        return self._lib.paia_gemv_pick_variant({"bf16": 0, "fp8": 1, "int4": 2}[kind], N, K)
+        """Library's per-shape variant: kind 'bf16' | 'fp8' | 'int4' | 'int4zp' (an index of variants_int4)."""
+        return self._lib.paia_gemv_pick_variant({"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[kind], N, K)
 
     def build_info(self):
         return self._lib.paia_gemv_build_info().decode()

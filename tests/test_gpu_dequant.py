@@ -79,7 +79,7 @@ def test_torch_ops_match_c_abi(oracle, gemv_lib, cuda):
                         ("int4zp", (4608, 3584))]:
         o, _ = make(fmt, N, K, bias=fmt in ("bf16", "fp8", "int4zp"))
         d = to_device(o, cuda)
-        kind = "int4" if fmt.startswith("int4") else fmt
+        kind = fmt
         vid = gemv_lib.pick_variant(kind, N, K)
         note(f"torch op {fmt}")
         want = bits16(run_gemv(gemv_lib, fmt, d, vid))

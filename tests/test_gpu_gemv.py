@@ -73,7 +73,7 @@ def test_every_variant_on_awkward_shapes(oracle, gemv_lib, cuda, fmt):
 def test_real_shapes_picked_and_default_variant(oracle, gemv_lib, cuda, fmt):
     """The library's per-shape variant and the harness default, on every real and BASELINE projection shape."""
     kmult = {"bf16": 8, "fp8": 16}.get(fmt, 128)
-    kind = "int4" if fmt.startswith("int4") else fmt
+    kind = fmt
     default = {"bf16": (2, 4, 4, 0, 1), "fp8": (2, 2, 4, 0, 1)}.get(fmt, (4, 2, 4, 0, 1))
     vdef = next(v["id"] for v in variants(gemv_lib, fmt) if (v["R"], v["U"], v["W"], v["S"], v["H"]) == default)
     for N, K in sorted(set(REAL + BASELINE_SHAPES)):
@@ -120,7 +120,7 @@ def column_dequant(O, fmt, np_ops, k):
 def test_unit_vector_exact_full_size(oracle, gemv_lib, cuda, fmt):
     """Size-independent exact check at every BASELINE shape: x = e_k gives y = bf16(deq(W[:, k])) in every row
     (every row index, the chunk and group holding k, the K tail and the epilogue are all exercised)."""
-    kind = "int4" if fmt.startswith("int4") else fmt
+    kind = fmt
     shapes = BASELINE_SHAPES + ([(128256, 4096)] if fmt == "bf16" else [])
     for N, K in shapes:
         ops, np_ops = make(fmt, N, K)
@@ -219,7 +219,7 @@ def test_graph_capture_replays_match_eager(oracle, gemv_lib, cuda):
                         ("int4zp", (4608, 3584))]:
         ops, np_ops = make(fmt, N, K, bias=fmt != "int4")
         dev = to_device(ops, cuda)
-        kind = "int4" if fmt.startswith("int4") else fmt
+        kind = fmt
         vid = gemv_lib.pick_variant(kind, N, K)
         eager = bits16(run_gemv(gemv_lib, fmt, dev, vid))
         cases.append((fmt, dev, vid, eager, torch.empty(N, dtype=torch.bfloat16, device=cuda)))

@@ -1,0 +1,105 @@
+"""Benchmark-harness logic without a GPU: the CPU reference the harness gates on, the rocprofv3 summaries, the tuned
+per-shape table and bench.py's one-GPU contract."""
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from paia_bench import pmc, rocprof_summary
+from paia_bench.cases import GemvCase
+from paia_bench.inputs import as_numpy, make_operands
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+class _NoLib:
+    def pick_variant(self, kind, N, K):
+        return 0
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
+def test_harness_reference_matches_oracle(oracle, fmt):
+    """GemvCase.reference (torch dequant + fp32 matmul, the reference harness's method) agrees with the fp64 oracle
+    to fp32 accuracy, on all rows and on a row subset, with and without bias."""
+    for N, K, bias in [(37, 256, False), (64, 3584, fmt != "int4")]:
+        c = GemvCase(_NoLib(), fmt, N, K, bias=bias)
+        c.ops0 = make_operands(fmt, N, K, bias=bias)
+        a = as_numpy(c.ops0)
+        b = a.get("bias")
+        ref64 = {"bf16": lambda: oracle.gemv_bf16_f64(a["W"], a["x"], b),
+                 "fp8": lambda: oracle.gemv_fp8_f64(a["Wq"], a["scale"], a["x"], b),
+                 "int4": lambda: oracle.gemv_int4_f64(a["Wq"], a["scales"], a["x"]),
+                 "int4zp": lambda: oracle.gemv_int4_zp_f64(a["Wq"], a["scales"], a["zeros"], a["x"], b)}[fmt]()
+        got = c.reference().numpy().astype(np.float64)
+        assert np.allclose(got, ref64, rtol=1e-5, atol=1e-5 * np.abs(ref64).max())
+        rows = [0, N // 2, N - 1]
+        # (BLAS blocking differs with the row count: equal to fp32 rounding, not bit for bit)
+        assert np.allclose(c.reference(rows).numpy(), c.reference().numpy()[rows], rtol=1e-6, atol=1e-6)
+
+
+def _counter_csv(path, rows):
+    cols = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    with open(path, "w") as f:
+        f.write(",".join(f'"{c}"' for c in cols) + "\n")
+        for i, (k, c, v) in enumerate(rows):
+            f.write(f'{i},"{k}","{c}",{v}\n')
+
+
+def test_pmc_summary_calibrates_counters(tmp_path):
+    """FETCH_SIZE/WRITE_SIZE (KiB per dispatch) are scaled by what they read for the calibration kernels: a counter
+    that reads half the bytes of the known-size read probe is doubled for the GEMV too."""
+    cal_kib = pmc.CAL_BYTES / 1024
+    k = "void paia::gemv_kernel<1, 2, 2, 4, 2, false>(paia::GemvParams)"
+    fetch, write = tmp_path / "f.csv", tmp_path / "w.csv"
+    _counter_csv(fetch, [("read_probe_kernel<1>", "FETCH_SIZE", cal_kib / 2), ("copy_probe_kernel", "FETCH_SIZE",
+                                                                              cal_kib / 2),
+                         (k, "FETCH_SIZE", 57863.0), (k, "FETCH_SIZE", 57860.0), (k, "FETCH_SIZE", 57870.0)])
+    _counter_csv(write, [("read_probe_kernel<1>", "WRITE_SIZE", 0.0), ("copy_probe_kernel", "WRITE_SIZE", cal_kib),
+                         (k, "WRITE_SIZE", 224.0)])
+    out = tmp_path / "t.json"
+    pmc.main(["summarize", "--fetch", str(fetch), "--write", str(write), "--out", str(out), "--case", "c1",
+              "--fmt", "fp8", "--shape", "28672x4096"])
+    d = json.loads(out.read_text())
+    assert d["calibration"]["fetch_per_byte_read_probe"] == 0.5
+    e = d["cases"]["c1"]
+    assert e["fetch_bytes"] == round(57863.0 * 1024 * 2) and e["write_bytes"] == 224 * 1024
+    assert e["algorithmic_bytes"] == 117620736 and e["kernel"] == "paia::gemv_kernel<1, 2, 2, 4, 2, false>"
+
+
+def test_rocprof_trace_summary_groups_by_grid(tmp_path):
+    t = tmp_path / "trace.csv"
+    cols = ["Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp", "End_Timestamp", "VGPR_Count",
+            "SGPR_Count", "LDS_Block_Size", "Scratch_Size"]
+    k = "void paia::gemv_kernel<1, 2, 2, 4, 2, false>(paia::GemvParams)"
+    rows = [(k, 256 * 1024, 256, 0, 1000), (k, 256 * 1024, 256, 0, 3000), (k, 512 * 1024, 512, 0, 5000),
+            ("other", 64, 64, 0, 9)]
+    with open(t, "w") as f:
+        f.write(",".join(cols) + "\n")
+        for r in rows:
+            f.write(f'"{r[0]}",{r[1]},{r[2]},{r[3]},{r[4]},40,64,0,0\n')
+    s = rocprof_summary.summarize(str(t), "gemv_kernel")
+    assert [(r["blocks"], r["threads"], r["calls"], r["avg_ns"]) for r in s] == [(1024, 512, 1, 5000.0), (1024, 256, 2, 2000.0)]
+    assert "paia::gemv_kernel<1, 2, 2, 4, 2, false>" in rocprof_summary.to_markdown(s)
+
+
+def test_tuned_table_drives_pick_variant(gemv_lib):
+    """Every entry of the frozen MI355X table is what paia_gemv_pick_variant returns for that shape."""
+    tuned = json.loads((ROOT / "paia-project_amd" / "tuned" / "mi355x.json").read_text())
+    fams = {"shapes": ("bf16", gemv_lib.variants), "fp8_shapes": ("fp8", gemv_lib.variants_fp8),
+            "int4_shapes": ("int4", gemv_lib.variants_int4), "int4zp_shapes": ("int4zp", gemv_lib.variants_int4)}
+    n = 0
+    for sec, (kind, fam) in fams.items():
+        for key, e in tuned.get(sec, {}).items():
+            N, K = map(int, key.split("x"))
+            v = fam[gemv_lib.pick_variant(kind, N, K)]
+            assert all(v[k] == e["variant"][k] for k in "RUWH"), (sec, key, v, e["variant"])
+            n += 1
+    assert n >= 30
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr

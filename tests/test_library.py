@@ -50,8 +50,8 @@ def test_variant_tables_hold_harness_defaults(gemv_lib):
     assert has(gemv_lib.variants_int4, {"R": 4, "U": 2, "W": 4, "S": 0, "H": 1})
     keys = {(v["R"], v["U"], v["W"], v["S"], v["H"]) for v in gemv_lib.variants}
     assert len(keys) == 96                                               # tuples are unique
-    for kind in ("bf16", "fp8", "int4"):
-        n = {"bf16": 96, "fp8": 36, "int4": 48}[kind]
+    for kind in ("bf16", "fp8", "int4", "int4zp"):
+        n = {"bf16": 96, "fp8": 36, "int4": 48, "int4zp": 48}[kind]
         for N, K in [(4096, 4096), (6144, 4096), (3584, 18944), (1, 128)]:
             assert 0 <= gemv_lib.pick_variant(kind, N, K) < n
 
