@@ -81,6 +81,20 @@ PAIA_API int paia_dequant_int4(const void* Wq, const void* scales, void* out, in
 PAIA_API int paia_dequant_int4_zp(const void* Wq, const void* scales, const void* zeros, void* out, int N, int K,
                                   void* stream);
 
+/* ---- on-device quantizers from fp32 W [N][K] row-major (no reference C symbol: the reference quantizes with torch,
+ *      src/paia_gemv/quant.py:8-31; same values as quant.py / quant_host.h:74-106). W 16-byte aligned. ------------ */
+/* q e4m3fn [N][K] (16-byte aligned), scale fp32 [N]: scale = amax/448 (1 for a zero row), q = e4m3_rn(clamp(w/scale,
+ * +-448)). K % 16 == 0. Replaces torch quantize_fp8_rowwise (src/paia_gemv/quant.py:8-13). */
+PAIA_API int paia_quantize_fp8_rowwise(const void* W, void* q, void* scale, int N, int K, void* stream);
+/* packed [N][K/2] (16-byte aligned), scales fp16 [N][K/128]: s = f16(amax/7) (1 for a zero group, 1 where it
+ * underflows), n = clamp(rint(w/s), -7, 7) + 8. K % 128 == 0. Replaces torch quantize_int4_g128 (quant.py:20-31). */
+PAIA_API int paia_quantize_int4_g128(const void* W, void* packed, void* scales, int N, int K, void* stream);
+/* no reference counterpart (asymmetric INT4 of the BASELINE configs): per group of 128, lo = min(0, min w),
+ * hi = max(0, max w), s = bf16((hi - lo)/15) (1 if 0), z = clamp(rint(-lo/s), 0, 15), q = clamp(rint(w/s) + z, 0, 15);
+ * packed [N][K/2], scales bf16 [N][G], zeros [N][ceil(G/2)] (group 2j low nibble). K % 128 == 0. */
+PAIA_API int paia_quantize_int4_zp_g128(const void* W, void* packed, void* scales, void* zeros, int N, int K,
+                                        void* stream);
+
 /* no reference counterpart (the reference picks variants in Python from src/tuned/<platform>.json,
  * paia-bench/bench/ops/ours_bf16.py:32-38): the library's per-shape variant for kind 0 BF16, 1 FP8, 2 INT4 reference
  * format, 3 INT4 asymmetric (an index of the paia_gemv_int4 table). Always returns a valid index of that table. */

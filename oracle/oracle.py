@@ -61,6 +61,7 @@ def lib():
         L.po_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.po_quantize_fp8_rowwise.argtypes = [_f32p, _int, _int, _u8p, _f32p]
         L.po_quantize_int4_g128.argtypes = [_f32p, _int, _int, _u8p, _u16p]
+        L.po_quantize_int4_zp_g128.argtypes = [_f32p, _int, _int, _u8p, _u16p, _u8p]
         L.po_dequant_fp8.argtypes = [_u8p, _f32p, _int, _int, _f32p]
         L.po_dequant_int4.argtypes = [_u8p, _u16p, _int, _int, _f32p]
         L.po_dequant_int4_zp.argtypes = [_u8p, _u16p, _u8p, _int, _int, _f32p]
@@ -176,6 +177,20 @@ def quantize_int4_g128(W):
     s = np.empty((N, K // 128), np.uint16)
     lib().po_quantize_int4_g128(W, N, K, p, s)
     return p, s
+
+
+def quantize_int4_zp_g128(W):
+    """W fp32 [N,K] -> asymmetric INT4 (packed uint8 [N,K/2], scales bf16 bits uint16 [N,G], zeros uint8
+    [N,ceil(G/2)]). No reference code: the closed form of paia_oracle.c, pinned by tests/test_oracle.py."""
+    W = _c(W, np.float32)
+    N, K = W.shape
+    assert K % 128 == 0
+    G = K // 128
+    p = np.empty((N, K // 2), np.uint8)
+    s = np.empty((N, G), np.uint16)
+    z = np.empty((N, (G + 1) // 2), np.uint8)
+    lib().po_quantize_int4_zp_g128(W, N, K, p, s, z)
+    return p, s, z
 
 
 def dequant_fp8(q, scale):

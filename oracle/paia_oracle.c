@@ -150,6 +150,42 @@ void po_quantize_int4_g128(const float* W, int N, int K, uint8_t* packed, uint16
     }
 }
 
+/* Asymmetric INT4 g128 (no reference code; the format of the BASELINE INT4 configs, dequant (q - z) * s): per group,
+ * lo = min(0, min w), hi = max(0, max w), s = bf16_rn((hi - lo) / 15) (bf16 1.0 if that is 0),
+ * z = clamp(rint(-lo / s), 0, 15), q = clamp(rint(w / s) + z, 0, 15). zeros [N][ceil(G/2)], group 2j low nibble. */
+void po_quantize_int4_zp_g128(const float* W, int N, int K, uint8_t* packed, uint16_t* scales_bf16, uint8_t* zeros)
+{
+    const int G = K / 128, ZB = (G + 1) / 2;
+    for (int n = 0; n < N; ++n) {
+        for (int j = 0; j < ZB; ++j) zeros[(size_t)n * (size_t)ZB + (size_t)j] = 0;
+        for (int g = 0; g < G; ++g) {
+            const float* w = W + (size_t)n * (size_t)K + (size_t)g * 128u;
+            float lo = 0.0f, hi = 0.0f;
+            for (int i = 0; i < 128; ++i) {
+                if (w[i] < lo) lo = w[i];
+                if (w[i] > hi) hi = w[i];
+            }
+            uint16_t sb = po_f32_to_bf16((hi - lo) / 15.0f);
+            float s = po_bf16_to_f32(sb);
+            if (!(s > 0.0f)) {
+                sb = 0x3F80u;
+                s = 1.0f;
+            }
+            float zf = rintf(-lo / s);
+            zf = zf < 0.0f ? 0.0f : (zf > 15.0f ? 15.0f : zf);
+            scales_bf16[(size_t)n * (size_t)G + (size_t)g] = sb;
+            zeros[(size_t)n * (size_t)ZB + (size_t)(g >> 1)] |= (uint8_t)((unsigned)zf << ((g & 1) * 4));
+            uint8_t* dst = packed + (size_t)n * (size_t)(K / 2) + (size_t)g * 64u;
+            for (int i = 0; i < 64; ++i) {
+                float a = rintf(w[2 * i] / s) + zf, b = rintf(w[2 * i + 1] / s) + zf;
+                a = a < 0.0f ? 0.0f : (a > 15.0f ? 15.0f : a);
+                b = b < 0.0f ? 0.0f : (b > 15.0f ? 15.0f : b);
+                dst[i] = (uint8_t)((unsigned)a | ((unsigned)b << 4));
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------------------------------------------- */
 /* dequantizers                                                                                                    */
 /* ------------------------------------------------------------------------------------------------------------- */

@@ -35,6 +35,8 @@ float po_bf16_to_f32(uint16_t b);
 /* ---- quantizers (W is N x K row-major fp32) ---- */
 void po_quantize_fp8_rowwise(const float* W, int N, int K, uint8_t* q, float* scale);
 void po_quantize_int4_g128(const float* W, int N, int K, uint8_t* packed, uint16_t* scales_f16);
+/* asymmetric INT4 (no reference code): min/max per group, bf16 scale, 4-bit zero point, (q - z) * s */
+void po_quantize_int4_zp_g128(const float* W, int N, int K, uint8_t* packed, uint16_t* scales_bf16, uint8_t* zeros);
 
 /* ---- dequantizers to fp32 [N][K] (bit-exact definitions) ---- */
 void po_dequant_fp8(const uint8_t* q, const float* scale, int N, int K, float* out);

@@ -198,6 +198,68 @@ at::Tensor dequant_int4_zp(const at::Tensor& Wq, const at::Tensor& scales, const
     return out;
 }
 
+// ---- quantizers (fp32 W [N, K] on the device) ----------------------------------------------------------------
+void check_w32(const at::Tensor& W, int64_t kmult)
+{
+    TORCH_CHECK(W.dim() == 2 && W.scalar_type() == at::kFloat && W.is_contiguous(), "W must be contiguous fp32 [N, K]");
+    TORCH_CHECK(W.size(1) % kmult == 0, "K must be a multiple of ", kmult);
+}
+
+std::tuple<at::Tensor, at::Tensor> quantize_fp8_rowwise(const at::Tensor& W)
+{
+    check_w32(W, 16);
+    const int64_t N = W.size(0), K = W.size(1);
+    at::Tensor q = at::empty({N, K}, W.options().dtype(at::kByte));
+    at::Tensor scale = at::empty({N}, W.options());
+    c10::DeviceGuard g(W.device());
+    check_rc(paia_quantize_fp8_rowwise(W.data_ptr(), q.data_ptr(), scale.data_ptr(), (int)N, (int)K, stream_of(W)),
+             "paia_quantize_fp8_rowwise");
+    return {q, scale};
+}
+
+std::tuple<at::Tensor, at::Tensor> quantize_int4_g128(const at::Tensor& W)
+{
+    check_w32(W, 128);
+    const int64_t N = W.size(0), K = W.size(1);
+    at::Tensor packed = at::empty({N, K / 2}, W.options().dtype(at::kByte));
+    at::Tensor scales = at::empty({N, K / 128}, W.options().dtype(at::kHalf));
+    c10::DeviceGuard g(W.device());
+    check_rc(paia_quantize_int4_g128(W.data_ptr(), packed.data_ptr(), scales.data_ptr(), (int)N, (int)K, stream_of(W)),
+             "paia_quantize_int4_g128");
+    return {packed, scales};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> quantize_int4_zp_g128(const at::Tensor& W)
+{
+    check_w32(W, 128);
+    const int64_t N = W.size(0), K = W.size(1), G = K / 128;
+    at::Tensor packed = at::empty({N, K / 2}, W.options().dtype(at::kByte));
+    at::Tensor scales = at::empty({N, G}, W.options().dtype(at::kBFloat16));
+    at::Tensor zeros = at::empty({N, (G + 1) / 2}, W.options().dtype(at::kByte));
+    c10::DeviceGuard g(W.device());
+    check_rc(paia_quantize_int4_zp_g128(W.data_ptr(), packed.data_ptr(), scales.data_ptr(), zeros.data_ptr(), (int)N,
+                                        (int)K, stream_of(W)),
+             "paia_quantize_int4_zp_g128");
+    return {packed, scales, zeros};
+}
+
+std::tuple<at::Tensor, at::Tensor> quantize_fp8_rowwise_meta(const at::Tensor& W)
+{
+    return {at::empty({W.size(0), W.size(1)}, W.options().dtype(at::kByte)), at::empty({W.size(0)}, W.options())};
+}
+std::tuple<at::Tensor, at::Tensor> quantize_int4_g128_meta(const at::Tensor& W)
+{
+    return {at::empty({W.size(0), W.size(1) / 2}, W.options().dtype(at::kByte)),
+            at::empty({W.size(0), W.size(1) / 128}, W.options().dtype(at::kHalf))};
+}
+std::tuple<at::Tensor, at::Tensor, at::Tensor> quantize_int4_zp_g128_meta(const at::Tensor& W)
+{
+    const int64_t G = W.size(1) / 128;
+    return {at::empty({W.size(0), W.size(1) / 2}, W.options().dtype(at::kByte)),
+            at::empty({W.size(0), G}, W.options().dtype(at::kBFloat16)),
+            at::empty({W.size(0), (G + 1) / 2}, W.options().dtype(at::kByte))};
+}
+
 // ---- Meta (shape-only) kernels ------------------------------------------------------------------------------
 at::Tensor gemv_bf16_meta(const at::Tensor& W, const at::Tensor& x, const std::optional<at::Tensor>&, int64_t)
 {
@@ -252,6 +314,9 @@ TORCH_LIBRARY(paia_gemv, m)
     m.def("dequant_fp8(Tensor Wq, Tensor scale) -> Tensor");
     m.def("dequant_int4(Tensor Wq, Tensor scales) -> Tensor");
     m.def("dequant_int4_zp(Tensor Wq, Tensor scales, Tensor zeros) -> Tensor");
+    m.def("quantize_fp8_rowwise(Tensor W) -> (Tensor, Tensor)");
+    m.def("quantize_int4_g128(Tensor W) -> (Tensor, Tensor)");
+    m.def("quantize_int4_zp_g128(Tensor W) -> (Tensor, Tensor, Tensor)");
 }
 
 // torch on ROCm dispatches HIP tensors under the CUDA key.
@@ -268,6 +333,9 @@ TORCH_LIBRARY_IMPL(paia_gemv, CUDA, m)
     m.impl("dequant_fp8", &dequant_fp8);
     m.impl("dequant_int4", &dequant_int4);
     m.impl("dequant_int4_zp", &dequant_int4_zp);
+    m.impl("quantize_fp8_rowwise", &quantize_fp8_rowwise);
+    m.impl("quantize_int4_g128", &quantize_int4_g128);
+    m.impl("quantize_int4_zp_g128", &quantize_int4_zp_g128);
 }
 
 TORCH_LIBRARY_IMPL(paia_gemv, Meta, m)
@@ -283,4 +351,7 @@ TORCH_LIBRARY_IMPL(paia_gemv, Meta, m)
     m.impl("dequant_fp8", &dequant_fp8_meta);
     m.impl("dequant_int4", &dequant_int4_meta);
     m.impl("dequant_int4_zp", &dequant_int4_zp_meta);
+    m.impl("quantize_fp8_rowwise", &quantize_fp8_rowwise_meta);
+    m.impl("quantize_int4_g128", &quantize_int4_g128_meta);
+    m.impl("quantize_int4_zp_g128", &quantize_int4_zp_g128_meta);
 }

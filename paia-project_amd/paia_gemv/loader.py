@@ -6,7 +6,8 @@ Drop-in for src/paia_gemv/loader.py:12-109: same `find_lib`, `current_raw_stream
 torch's current stream, so calls can be captured into a HIP graph (torch.cuda.CUDAGraph on ROCm).
 
 Additions for the gfx950 build: `bf16_bias`, `fp8_bias`, `int4_zp` (asymmetric INT4 with optional bias),
-`dequant_fp8`, `dequant_int4`, `dequant_int4_zp`, `pick_variant`, `build_info`.
+`dequant_fp8`, `dequant_int4`, `dequant_int4_zp`, `quantize_fp8_rowwise`, `quantize_int4_g128`,
+`quantize_int4_zp_g128`, `pick_variant`, `build_info`.
 """
 from __future__ import annotations
 
@@ -58,6 +59,9 @@ class GemvLib:
             "paia_dequant_fp8": [_P, _P, _P, _I, _I, _P],
             "paia_dequant_int4": [_P, _P, _P, _I, _I, _P],
             "paia_dequant_int4_zp": [_P, _P, _P, _P, _I, _I, _P],
+            "paia_quantize_fp8_rowwise": [_P, _P, _P, _I, _I, _P],
+            "paia_quantize_int4_g128": [_P, _P, _P, _I, _I, _P],
+            "paia_quantize_int4_zp_g128": [_P, _P, _P, _P, _I, _I, _P],
             "paia_gemv_pick_variant": [_I, _I, _I],
             "paia_gemv_bf16_variant_count": [],
             "paia_gemv_bf16_variant_info": [_I] + [ctypes.POINTER(_I)] * 5,
@@ -153,6 +157,21 @@ class GemvLib:
     def dequant_int4_zp(self, Wq_ptr, scales_ptr, zeros_ptr, out_ptr, N, K, stream=None):
         self._check(self._lib.paia_dequant_int4_zp(Wq_ptr, scales_ptr, zeros_ptr, out_ptr, N, K, self._st(stream)),
                     "paia_dequant_int4_zp")
+
+    def quantize_fp8_rowwise(self, W_ptr, q_ptr, scale_ptr, N, K, stream=None):
+        """fp32 W [N,K] -> e4m3 q [N,K], fp32 scale [N] on the device (quant.py:8-13 semantics)."""
+        self._check(self._lib.paia_quantize_fp8_rowwise(W_ptr, q_ptr, scale_ptr, N, K, self._st(stream)),
+                    "paia_quantize_fp8_rowwise")
+
+    def quantize_int4_g128(self, W_ptr, packed_ptr, scales_ptr, N, K, stream=None):
+        """fp32 W [N,K] -> packed [N,K/2], fp16 scales [N,K/128] on the device (quant.py:20-31 semantics)."""
+        self._check(self._lib.paia_quantize_int4_g128(W_ptr, packed_ptr, scales_ptr, N, K, self._st(stream)),
+                    "paia_quantize_int4_g128")
+
+    def quantize_int4_zp_g128(self, W_ptr, packed_ptr, scales_ptr, zeros_ptr, N, K, stream=None):
+        """fp32 W [N,K] -> asymmetric INT4: packed [N,K/2], bf16 scales [N,G], zeros [N,ceil(G/2)] on the device."""
+        self._check(self._lib.paia_quantize_int4_zp_g128(W_ptr, packed_ptr, scales_ptr, zeros_ptr, N, K,
+                                                         self._st(stream)), "paia_quantize_int4_zp_g128")
 
     def pick_variant(self, kind, N, K):
         """Library's per-shape variant: kind 'bf16' | 'fp8' | 'int4' | 'int4zp' (an index of variants_int4)."""

@@ -85,3 +85,21 @@ def dequant_int4(Wq, scales):
 def dequant_int4_zp(Wq, scales, zeros):
     load()
     return torch.ops.paia_gemv.dequant_int4_zp(Wq, scales, zeros)
+
+
+def quantize_fp8_rowwise(W):
+    """fp32 W [N,K] on the device -> (q uint8 e4m3 [N,K], scale fp32 [N]) by the HIP quantizer."""
+    load()
+    return torch.ops.paia_gemv.quantize_fp8_rowwise(W)
+
+
+def quantize_int4_g128(W):
+    """fp32 W [N,K] on the device -> (packed uint8 [N,K/2], scales fp16 [N,K/128]) by the HIP quantizer."""
+    load()
+    return torch.ops.paia_gemv.quantize_int4_g128(W)
+
+
+def quantize_int4_zp_g128(W):
+    """fp32 W [N,K] on the device -> asymmetric INT4 (packed [N,K/2], scales bf16 [N,G], zeros [N,ceil(G/2)])."""
+    load()
+    return torch.ops.paia_gemv.quantize_int4_zp_g128(W)

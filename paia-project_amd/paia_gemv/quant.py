@@ -6,10 +6,13 @@ Same API and semantics as src/paia_gemv/quant.py:8-38 (the reference's formats, 
   INT4 W4A16 unsigned nibbles, zero point 8, group 128 along K, fp16 scale = fp16(amax/7) (1 if zero);
              n = clamp(rint(w/s), -7, 7) + 8 with s = float(scale) (1 where the fp16 scale underflowed to 0);
              byte j of a row = weight 2j (low nibble) | weight 2j+1 (high nibble).
-These torch functions are the format definitions the harness checks against; the HIP kernels dequantise in
-registers, and `paia_gemv.ops.dequant_*` runs the same dequantisation on the GPU.
+The quantizers run the library's HIP kernels for a tensor on the GPU (paia_gemv.ops.quantize_*, bit-identical to
+these definitions; they raise if the extension is missing) and the torch definitions below for a CPU tensor. The
+dequantisers are the torch definitions on either device (paia_gemv.ops.dequant_* runs them as HIP kernels).
 
 Additions for the asymmetric INT4 format of the BASELINE configurations (no reference counterpart):
+  `quantize_int4_zp_g128(W)` per group of 128: lo = min(0, min w), hi = max(0, max w), s = bf16((hi - lo) / 15)
+                            (1 if that is 0), z = clamp(rint(-lo / s), 0, 15), q = clamp(rint(w / s) + z, 0, 15)
   `pack_int4(q)`            q uint8 [N,K] in 0..15 -> packed uint8 [N,K/2] (same nibble order as above)
   `pack_zeros(z)`           z uint8 [N,G] in 0..15 -> uint8 [N,ceil(G/2)], group 2j low nibble, 2j+1 high
   `dequant_int4_zp(p, s, z)` (q - z) * float(s_bf16), fp32 [N,K]
@@ -19,6 +22,9 @@ import torch
 
 def quantize_fp8_rowwise(W):
     """W [N,K] float32 -> (q uint8 [N,K], scale float32 [N])."""
+    if W.is_cuda:
+        from . import ops
+        return ops.quantize_fp8_rowwise(W.float().contiguous())
     amax = W.abs().amax(dim=1)
     scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax)).float()
     q = (W / scale[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
@@ -35,6 +41,9 @@ def quantize_int4_g128(W):
     N, K = W.shape
     if K % 128:
         raise ValueError("K % 128 required")
+    if W.is_cuda:
+        from . import ops
+        return ops.quantize_int4_g128(W.float().contiguous())
     grp = W.reshape(N, K // 128, 128)
     amax = grp.abs().amax(dim=-1)
     s16 = torch.where(amax > 0, amax / 7.0, torch.ones_like(amax)).to(torch.float16)
@@ -48,6 +57,26 @@ def dequant_int4(packed, s16):
     """(n - 8) * float(s16) -> fp32 [N,K]."""
     n = unpack_int4(packed).float()
     return (n - 8.0) * s16.float().repeat_interleave(128, dim=1)
+
+
+def quantize_int4_zp_g128(W):
+    """W [N,K] float32, K % 128 == 0 -> (packed uint8 [N,K/2], scales bf16 [N,G], zeros uint8 [N,ceil(G/2)]),
+    dequantising as (q - z) * s."""
+    N, K = W.shape
+    if K % 128:
+        raise ValueError("K % 128 required")
+    if W.is_cuda:
+        from . import ops
+        return ops.quantize_int4_zp_g128(W.float().contiguous())
+    grp = W.float().reshape(N, K // 128, 128)
+    lo = grp.amin(dim=-1).clamp(max=0.0)
+    hi = grp.amax(dim=-1).clamp(min=0.0)
+    sb = ((hi - lo) / 15.0).to(torch.bfloat16)
+    sb = torch.where(sb.float() > 0, sb, torch.ones_like(sb))
+    s = sb.float()
+    z = torch.round(-lo / s).clamp(0, 15)
+    q = (torch.round(grp / s[..., None]) + z[..., None]).clamp(0, 15).to(torch.uint8).reshape(N, K)
+    return pack_int4(q), sb.contiguous(), pack_zeros(z.to(torch.uint8))
 
 
 def pack_int4(q):

@@ -87,6 +87,12 @@ def test_contract_return_codes_without_launch(gemv_lib):
     assert L.paia_dequant_fp8(A, A, A, 4, 8, None) == -2
     assert L.paia_dequant_int4(A, A, A + 4, 4, 128, None) == -2
     assert L.paia_dequant_int4_zp(A, A, None, A, 4, 128, None) == -2
+    assert L.paia_quantize_fp8_rowwise(A, A, A, 4, 24, None) == -2            # K % 16
+    assert L.paia_quantize_fp8_rowwise(A + 4, A, A, 4, 32, None) == -2        # W not 16-byte aligned
+    assert L.paia_quantize_int4_g128(A, A, A, 4, 64, None) == -2              # K % 128
+    assert L.paia_quantize_int4_g128(A, A, A + 1, 4, 128, None) == -2         # scales not 2-byte aligned
+    assert L.paia_quantize_int4_zp_g128(A, A, A, None, 4, 128, None) == -2    # zeros missing
+    assert L.paia_quantize_int4_zp_g128(A, A, A, A, 0, 128, None) == -2       # N <= 0
     # LDS limit of the gfx950 design: x is staged in 64 KiB
     assert L.paia_gemv_bf16(A, A, A, 4, 32768 + 8, 0, None) == -2
     assert L.paia_gemv_int4(A, A, A, A, 4, 30720 + 128, 0, None) == -2
@@ -118,7 +124,8 @@ def test_torch_ops_registered_and_meta_shapes():
     from paia_gemv import ops
     ops.load()
     names = ["gemv_bf16", "gemv_bf16_out", "gemv_fp8", "gemv_fp8_out", "gemv_int4", "gemv_int4_out",
-             "gemv_int4_zp", "gemv_int4_zp_out", "dequant_fp8", "dequant_int4", "dequant_int4_zp"]
+             "gemv_int4_zp", "gemv_int4_zp_out", "dequant_fp8", "dequant_int4", "dequant_int4_zp",
+             "quantize_fp8_rowwise", "quantize_int4_g128", "quantize_int4_zp_g128"]
     for n in names:
         assert hasattr(torch.ops.paia_gemv, n)
     m = torch.device("meta")
@@ -134,6 +141,13 @@ def test_torch_ops_registered_and_meta_shapes():
     d = torch.ops.paia_gemv.dequant_int4(torch.empty(N, K // 2, dtype=torch.uint8, device=m),
                                          torch.empty(N, 3, dtype=torch.float16, device=m))
     assert d.shape == (N, K) and d.dtype == torch.float32
+    Wm = torch.empty(N, 640, dtype=torch.float32, device=m)
+    q, sc = torch.ops.paia_gemv.quantize_fp8_rowwise(Wm)
+    assert q.shape == (N, 640) and q.dtype == torch.uint8 and sc.shape == (N,)
+    p, sc = torch.ops.paia_gemv.quantize_int4_g128(Wm)
+    assert p.shape == (N, 320) and sc.shape == (N, 5) and sc.dtype == torch.float16
+    p, sc, z = torch.ops.paia_gemv.quantize_int4_zp_g128(Wm)
+    assert sc.dtype == torch.bfloat16 and z.shape == (N, 3) and z.dtype == torch.uint8
 
 
 def test_byte_accounting_matches_baseline_table():

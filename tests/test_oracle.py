@@ -283,3 +283,63 @@ def test_close_to_ref_gate(oracle):
     y_bad = oracle.f32_to_bf16_bits(np.float32([1.0, -2.0, 0.5, 103.0]))
     ok, _, rel = oracle.close_to_ref(y_bad, ref)
     assert not ok and abs(rel - 0.03) < 1e-6
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# asymmetric INT4 quantizer (no reference code): pinned by closed forms, not by restating it
+# ---------------------------------------------------------------------------------------------------------------
+def _zp_groups(oracle, p, s, z, G):
+    q = np.stack([p & 0xF, p >> 4], axis=-1).reshape(p.shape[0], -1)
+    zz = np.stack([z & 0xF, z >> 4], axis=-1).reshape(z.shape[0], -1)[:, :G]
+    return q, zz, oracle.bf16_bits_to_f32(s).reshape(s.shape)
+
+
+def test_int4_zp_quantizer_recovers_constructed_groups(oracle):
+    """W built as (q - z) * s from bf16 s, z in 0..15 and codes that include 0 and 15 in every group is recovered
+    exactly: then lo = -z s, hi = (15 - z) s, (hi - lo) / 15 = s exactly and rint(w / s) + z = q."""
+    rng = np.random.default_rng(21)
+    N, K = 9, 640
+    G = K // 128
+    q = rng.integers(0, 16, (N, K))
+    q[:, 0::128], q[:, 1::128] = 0, 15
+    z = rng.integers(0, 16, (N, G))
+    sb = oracle.f32_to_bf16_bits(rng.uniform(1e-3, 1e-1, (N, G)).astype(np.float32))
+    s = oracle.bf16_bits_to_f32(sb)
+    W = ((q - np.repeat(z, 128, axis=1)) * np.repeat(s, 128, axis=1)).astype(np.float32)
+    p2, s2, z2 = oracle.quantize_int4_zp_g128(W)
+    q2, zz2, _ = _zp_groups(oracle, p2, s2, z2, G)
+    assert np.array_equal(s2, sb) and np.array_equal(zz2, z) and np.array_equal(q2, q)
+
+
+def test_int4_zp_quantizer_roundtrip_bound_and_specials(oracle):
+    """Random groups: codes in 0..15 and |w - (q - z) s| <= s/2 (+ the bf16 rounding of s over 15 steps); an all-zero
+    group gives s = 1, z = 0, q = 0; a one-sided group keeps 0 representable (lo <= 0 <= hi)."""
+    rng = np.random.default_rng(22)
+    N, K = 7, 3584
+    G = K // 128
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[1, 256:384] = 0.0                                    # zero group
+    W[2, 0:128] = np.abs(W[2, 0:128])                      # positive-only group
+    p, sb, zp = oracle.quantize_int4_zp_g128(W)
+    q, z, s = _zp_groups(oracle, p, sb, zp, G)
+    deq = oracle.dequant_int4_zp(p, sb, zp)
+    sr = np.repeat(s, 128, axis=1)
+    assert np.all(np.abs(W - deq) <= sr * (0.5 + 15 * 2.0 ** -8) + 1e-12)
+    assert s[1, 2] == 1.0 and z[1, 2] == 0 and np.all(q[1, 256:384] == 0)
+    assert z[2, 0] == 0
+    assert zp.shape == (N, G // 2)
+    _, _, z3 = oracle.quantize_int4_zp_g128(W[:, :384])      # odd G = 3: the last byte's high nibble is padding 0
+    assert z3.shape == (N, 2) and np.all((z3[:, 1] >> 4) == 0)
+
+
+def test_int4_zp_quantizer_matches_torch_definition(oracle):
+    """The C restatement and the package's vectorised torch definition (paia_gemv.quant) agree bit for bit."""
+    import torch
+    from paia_gemv import quant
+    rng = np.random.default_rng(23)
+    for N, K in [(5, 384), (64, 4096), (3, 18944)]:
+        W = (rng.standard_normal((N, K)) * rng.uniform(1e-3, 1.0)).astype(np.float32)
+        p1, s1, z1 = oracle.quantize_int4_zp_g128(W)
+        p2, s2, z2 = quant.quantize_int4_zp_g128(torch.from_numpy(W))
+        assert np.array_equal(p1, p2.numpy()) and np.array_equal(z1, z2.numpy())
+        assert np.array_equal(s1, s2.view(torch.int16).numpy().view(np.uint16))
