@@ -100,6 +100,26 @@ PAIA_API int paia_quantize_int4_zp_g128(const void* W, void* packed, void* scale
  * format, 3 INT4 asymmetric (an index of the paia_gemv_int4 table). Always returns a valid index of that table. */
 PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
 
+/* ---- small batch: M = 1..16 activation rows on the matrix cores. No reference symbol: the reference's kernels are
+ * M = 1 only and M = 1..16 is its open item (src/README.md:118, swept by paia-bench/configs/shapes.yaml:63-64).
+ * x bf16 [M][K] row-major (16-byte aligned), y bf16 [M][N] row-major (2-byte aligned); the weight operands, their
+ * alignment and the K rules are those of the M = 1 entry point of the same format. bias bf16 [N] or NULL.
+ * kind: 0 BF16, 1 FP8, 2 INT4 reference format, 3 INT4 asymmetric. variant < 0 = paia_gemv_batch_pick_variant's.
+ * Knobs: P tiles of 16 rows per wave, U k-blocks of 128 columns in flight per wave, W waves per block, S waves
+ * sharing a tile along K. Returns 0, -1 bad variant, -2 bad shape/alignment (or M*S too large for the variant's LDS
+ * chunk), > 0 hipError_t. */
+PAIA_API int paia_gemv_batch_variant_count(int kind);
+PAIA_API int paia_gemv_batch_variant_info(int kind, int v, int* P, int* U, int* W, int* S);
+PAIA_API int paia_gemv_batch_pick_variant(int kind, int M, int N, int K);
+PAIA_API int paia_gemv_batch_bf16(const void* W, const void* x, const void* bias, void* y, int M, int N, int K,
+                                  int variant, void* stream);
+PAIA_API int paia_gemv_batch_fp8(const void* Wq, const void* scale, const void* x, const void* bias, void* y, int M,
+                                 int N, int K, int variant, void* stream);
+PAIA_API int paia_gemv_batch_int4(const void* Wq, const void* scales, const void* x, void* y, int M, int N, int K,
+                                  int variant, void* stream);
+PAIA_API int paia_gemv_batch_int4_zp(const void* Wq, const void* scales, const void* zeros, const void* x,
+                                     const void* bias, void* y, int M, int N, int K, int variant, void* stream);
+
 /* no reference counterpart: a human-readable build tag */
 PAIA_API const char* paia_gemv_build_info(void);
 

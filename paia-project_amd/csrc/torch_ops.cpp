@@ -7,6 +7,10 @@
 //
 // The reference reaches its kernels through ctypes only (src/paia_gemv/loader.py:28-99); these ops are the additional
 // Tensor-level surface (same semantics, same return-code errors surfaced as RuntimeError).
+//
+// x is [K], [1, K] or [M, K] with M <= 16 (y is [N], [1, N] or [M, N]). One activation row runs the M = 1 GEMV
+// kernels and `variant` indexes their table; M > 1 runs the small-batch matrix-core kernels (paia_gemv_batch_*) and
+// `variant` indexes the batch table of that format. -1 is the library's choice in both cases.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -32,24 +36,29 @@ void* stream_of(const at::Tensor& t)
     return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
 }
 
+constexpr int64_t kMaxRows = 16;   // activation rows the small-batch kernels take
+
 int64_t x_len(const at::Tensor& x)
 {
-    TORCH_CHECK(x.dim() == 1 || (x.dim() == 2 && x.size(0) == 1), "x must be [K] or [1, K] (M = 1 only)");
+    TORCH_CHECK(x.dim() == 1 || (x.dim() == 2 && x.size(0) >= 1 && x.size(0) <= kMaxRows),
+                "x must be [K] or [M, K] with 1 <= M <= 16");
     TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16");
     TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
     return x.size(-1);
 }
 
+int64_t x_rows(const at::Tensor& x) { return x.dim() == 2 ? x.size(0) : 1; }
+
 std::vector<int64_t> y_shape(const at::Tensor& x, int64_t N)
 {
-    if (x.dim() == 2) return {1, N};
+    if (x.dim() == 2) return {x.size(0), N};
     return {N};
 }
 
 void check_out(const at::Tensor& out, const at::Tensor& x, int64_t N)
 {
-    TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.is_contiguous() && out.numel() == N,
-                "out must be a contiguous bfloat16 tensor with N elements");
+    TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.is_contiguous() && out.numel() == x_rows(x) * N,
+                "out must be a contiguous bfloat16 tensor with M*N elements");
     TORCH_CHECK(out.device() == x.device(), "out must be on the device of x");
 }
 
@@ -75,6 +84,13 @@ void gemv_bf16_out(const at::Tensor& W, const at::Tensor& x, const std::optional
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
     c10::DeviceGuard g(W.device());
+    const int64_t M = x_rows(x);
+    if (M > 1) {
+        check_rc(paia_gemv_batch_bf16(W.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(), (int)M, (int)N,
+                                      (int)K, (int)variant, stream_of(W)),
+                 "paia_gemv_batch_bf16");
+        return;
+    }
     check_rc(paia_gemv_bf16_bias(W.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(), (int)N, (int)K,
                                  pick(variant, kBF16, N, K), stream_of(W)),
              "paia_gemv_bf16");
@@ -95,6 +111,13 @@ void gemv_fp8_out(const at::Tensor& Wq, const at::Tensor& scale, const at::Tenso
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
     c10::DeviceGuard g(Wq.device());
+    const int64_t M = x_rows(x);
+    if (M > 1) {
+        check_rc(paia_gemv_batch_fp8(Wq.data_ptr(), scale.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(),
+                                     (int)M, (int)N, (int)K, (int)variant, stream_of(Wq)),
+                 "paia_gemv_batch_fp8");
+        return;
+    }
     check_rc(paia_gemv_fp8_bias(Wq.data_ptr(), scale.data_ptr(), x.data_ptr(), opt_ptr(bias, N), out.data_ptr(),
                                 (int)N, (int)K, pick(variant, kFP8, N, K), stream_of(Wq)),
              "paia_gemv_fp8");
@@ -125,6 +148,13 @@ void gemv_int4_out(const at::Tensor& Wq, const at::Tensor& scales, const at::Ten
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
     c10::DeviceGuard g(Wq.device());
+    const int64_t M = x_rows(x);
+    if (M > 1) {
+        check_rc(paia_gemv_batch_int4(Wq.data_ptr(), scales.data_ptr(), x.data_ptr(), out.data_ptr(), (int)M, (int)N,
+                                      (int)K, (int)variant, stream_of(Wq)),
+                 "paia_gemv_batch_int4");
+        return;
+    }
     check_rc(paia_gemv_int4(Wq.data_ptr(), scales.data_ptr(), x.data_ptr(), out.data_ptr(), (int)N, (int)K,
                             pick(variant, kINT4, N, K), stream_of(Wq)),
              "paia_gemv_int4");
@@ -147,6 +177,14 @@ void gemv_int4_zp_out(const at::Tensor& Wq, const at::Tensor& scales, const at::
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
     c10::DeviceGuard g(Wq.device());
+    const int64_t M = x_rows(x);
+    if (M > 1) {
+        check_rc(paia_gemv_batch_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), x.data_ptr(),
+                                         opt_ptr(bias, N), out.data_ptr(), (int)M, (int)N, (int)K, (int)variant,
+                                         stream_of(Wq)),
+                 "paia_gemv_batch_int4_zp");
+        return;
+    }
     check_rc(paia_gemv_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), x.data_ptr(), opt_ptr(bias, N),
                                out.data_ptr(), (int)N, (int)K, pick(variant, kINT4ZP, N, K), stream_of(Wq)),
              "paia_gemv_int4_zp");

@@ -39,6 +39,7 @@ def current_raw_stream():
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
+KINDS = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}
 
 
 class GemvLib:
@@ -65,6 +66,13 @@ class GemvLib:
             "paia_gemv_pick_variant": [_I, _I, _I],
             "paia_gemv_bf16_variant_count": [],
             "paia_gemv_bf16_variant_info": [_I] + [ctypes.POINTER(_I)] * 5,
+            "paia_gemv_batch_variant_count": [_I],
+            "paia_gemv_batch_variant_info": [_I, _I] + [ctypes.POINTER(_I)] * 4,
+            "paia_gemv_batch_pick_variant": [_I, _I, _I, _I],
+            "paia_gemv_batch_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+            "paia_gemv_batch_fp8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+            "paia_gemv_batch_int4": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+            "paia_gemv_batch_int4_zp": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
         }
         for name, argtypes in sig.items():
             fn = getattr(lib, name)
@@ -82,6 +90,14 @@ class GemvLib:
             R, U, W, S, H = (_I() for _ in range(5))
             assert lib.paia_gemv_bf16_variant_info(v, *map(ctypes.byref, (R, U, W, S, H))) == 0
             self.variants.append({"id": v, "R": R.value, "U": U.value, "W": W.value, "S": S.value, "H": H.value})
+        self.variants_batch = {}
+        for kind, k in KINDS.items():
+            vs = []
+            for v in range(lib.paia_gemv_batch_variant_count(k)):
+                P, U, W, S = (_I() for _ in range(4))
+                assert lib.paia_gemv_batch_variant_info(k, v, *map(ctypes.byref, (P, U, W, S))) == 0
+                vs.append({"id": v, "P": P.value, "U": U.value, "W": W.value, "S": S.value})
+            self.variants_batch[kind] = vs
 
     @staticmethod
     def _qvariants(lib, kind):
@@ -175,7 +191,28 @@ class GemvLib:
 
     def pick_variant(self, kind, N, K):
         """Library's per-shape variant: kind 'bf16' | 'fp8' | 'int4' | 'int4zp' (an index of variants_int4)."""
-        return self._lib.paia_gemv_pick_variant({"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[kind], N, K)
+        return self._lib.paia_gemv_pick_variant(KINDS[kind], N, K)
+
+    # ---- small batch (M = 1..16 activation rows, x [M,K] and y [M,N] bf16 row-major) -------------------------
+    def batch_pick_variant(self, kind, M, N, K):
+        """The library's default small-batch variant (an index of variants_batch[kind]); -1 if M is out of range."""
+        return self._lib.paia_gemv_batch_pick_variant(KINDS[kind], M, N, K)
+
+    def batch_bf16(self, W_ptr, x_ptr, bias_ptr, y_ptr, M, N, K, variant=-1, stream=None):
+        self._check(self._lib.paia_gemv_batch_bf16(W_ptr, x_ptr, bias_ptr, y_ptr, M, N, K, variant, self._st(stream)),
+                    "paia_gemv_batch_bf16")
+
+    def batch_fp8(self, Wq_ptr, scale_ptr, x_ptr, bias_ptr, y_ptr, M, N, K, variant=-1, stream=None):
+        self._check(self._lib.paia_gemv_batch_fp8(Wq_ptr, scale_ptr, x_ptr, bias_ptr, y_ptr, M, N, K, variant,
+                                                  self._st(stream)), "paia_gemv_batch_fp8")
+
+    def batch_int4(self, Wq_ptr, scales_ptr, x_ptr, y_ptr, M, N, K, variant=-1, stream=None):
+        self._check(self._lib.paia_gemv_batch_int4(Wq_ptr, scales_ptr, x_ptr, y_ptr, M, N, K, variant,
+                                                   self._st(stream)), "paia_gemv_batch_int4")
+
+    def batch_int4_zp(self, Wq_ptr, scales_ptr, zeros_ptr, x_ptr, bias_ptr, y_ptr, M, N, K, variant=-1, stream=None):
+        self._check(self._lib.paia_gemv_batch_int4_zp(Wq_ptr, scales_ptr, zeros_ptr, x_ptr, bias_ptr, y_ptr, M, N, K,
+                                                      variant, self._st(stream)), "paia_gemv_batch_int4_zp")
 
     def build_info(self):
         return self._lib.paia_gemv_build_info().decode()

@@ -1,8 +1,12 @@
 """Tensor-level API: torch.ops.paia_gemv.* custom ops (torch.library) backed by libpaia_gemv.so.
 
     from paia_gemv import ops
-    y = ops.gemv_fp8(Wq, scale, x)                 # x bf16 [K] or [1,K] -> y bf16 [N] or [1,N]
+    y = ops.gemv_fp8(Wq, scale, x)                 # x bf16 [K] or [M,K] (M <= 16) -> y bf16 [N] or [M,N]
     ops.gemv_int4_zp(Wq, s, z, x, bias=b, out=y)   # writes y, allocates nothing
+
+One activation row runs the M = 1 GEMV kernels (`variant` indexes GemvLib.variants / variants_fp8 / variants_int4);
+M = 2..16 rows run the small-batch matrix-core kernels (`variant` indexes GemvLib.variants_batch[fmt]); -1 is the
+library's choice.
 
 The ops are registered by libpaia_gemv_torch.so (csrc/torch_ops.cpp); they run on torch's current stream and are
 HIP-graph capturable. There is no fallback: if the extension is missing, `load()` raises.

@@ -1,0 +1,242 @@
+"""CPU emulation of the small-batch matrix-core kernel (paia-project_amd/csrc/gemv_batch.h), no GPU.
+
+Two things are pinned here, the way test_decode_emulation.py and test_geometry.py pin the M = 1 kernel:
+  * Operand mapping. For one 16-row tile and one 128-column k-block, every lane's registers are built exactly as the
+    kernel builds them (load i of lane group h = bytes 64i + 16h .. +15 of the row's k-block; the format's in-register
+    decode; A fragments read from the LDS image of x at step_col(j, h), INT4 columns permuted within each 8), and the
+    v_mfma_f32_16x16x32_bf16 contraction D[m][n] = sum_g sum_e A_lane(m, g)[e] * B_lane(n, g)[e] is applied. The
+    result must equal the dense product sum_k deq(W[n,k]) x[m,k] exactly (small integer-valued operands, fp64). A wrong
+    column offset, a swapped load or a decode/staging order mismatch fails it.
+  * Work decomposition. The launch plan (k-blocks, splits, LDS chunking, grid) and the per-wave loop are replayed for
+    many (M, N, K, P, U, W, S): every (tile, k-block) is consumed exactly once, reading the LDS chunk slot that holds
+    that k-block's x, every LDS access stays inside the launch's LDS size, and split-K partial slots never collide.
+The MFMA lane layout itself (A row l%16 / B column l%16 from k-group l/16; D rows 4(l/16)+v) is the CDNA4 ISA's; the
+GPU tests check the kernel's output against the oracle, which fails for any other layout.
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from test_decode_emulation import C43, i4_decode_pairs
+
+LDS = 65536
+KINDS = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}
+
+
+def step_col(fmt, j, h):
+    """gemv_batch.h step_col: first column (within the k-block) of MFMA step j for lane group h."""
+    if fmt == "bf16":
+        return 32 * j + 8 * h
+    if fmt == "fp8":
+        return 64 * (j >> 1) + 16 * h + 8 * (j & 1)
+    return 32 * h + 8 * j
+
+
+def bytes_kb(fmt):
+    return {"bf16": 256, "fp8": 128}.get(fmt, 64)
+
+
+def words(b16):
+    """16 bytes -> 4 little-endian uint32 words."""
+    return np.frombuffer(np.ascontiguousarray(b16, dtype=np.uint8).tobytes(), dtype="<u4")
+
+
+def b_fragment(fmt, row_bytes, h, j):
+    """The 8 bf16 values (as float) lane group h feeds MFMA step j from one weight row's k-block bytes."""
+    loads = [row_bytes[64 * i + 16 * h: 64 * i + 16 * h + 16] for i in range(bytes_kb(fmt) // 64)]
+    if fmt == "bf16":
+        w = words(loads[j])
+        return np.concatenate([O.bf16_bits_to_f32(np.array([v & 0xFFFF, v >> 16], dtype=np.uint16)) for v in w])
+    if fmt == "fp8":
+        w = words(loads[j >> 1])
+        d = w[2 * (j & 1): 2 * (j & 1) + 2]
+        tab = O.e4m3_table()
+        # fp8x2_to_bf16x2<false/true>: bytes (0,1) then (2,3) of each word, each the exact e4m3 value in bf16
+        return np.array([tab[(int(v) >> (8 * b)) & 0xFF] for v in d for b in range(4)], dtype=np.float64)
+    w = words(loads[0])[j]
+    pairs = i4_decode_pairs(np.uint32(w))
+    return np.concatenate([O.bf16_bits_to_f32(np.array([int(p) & 0xFFFF, int(p) >> 16], dtype=np.uint16))
+                           for p in pairs]).astype(np.float64)
+
+
+def lds_row(fmt, xrow):
+    """LDS image of one activation row's k-block (128 bf16 values as float): INT4 permutes each 8 to
+    (0, 2, 4, 6, 1, 3, 5, 7), the order x_put writes."""
+    if fmt in ("int4", "int4zp"):
+        perm = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+        return np.concatenate([xrow[8 * v + perm] for v in range(16)])
+    return xrow.copy()
+
+
+def emulate_tile(fmt, wbytes, x, zc=None, s=None):
+    """One tile (16 rows) x one k-block for M = x.shape[0] rows: registers -> MFMA contraction -> (INT4) group
+    correction. Rows m >= M of A repeat row 0, as the kernel's lane address does."""
+    M = x.shape[0]
+    lds = [lds_row(fmt, x[m]) for m in range(M)]
+    D = np.zeros((16, 16))
+    for j in range(4):
+        for g in range(4):
+            for m in range(16):
+                a = lds[m if m < M else 0][step_col(fmt, j, g): step_col(fmt, j, g) + 8]
+                for n in range(16):
+                    D[m, n] += float(np.dot(a, b_fragment(fmt, wbytes[n], g, j)))
+    if fmt in ("int4", "int4zp"):
+        xs = np.array([x[m if m < M else 0].sum() for m in range(16)])
+        D = s[None, :] * (D - zc[None, :] * xs[:, None])
+    return D[:M]
+
+
+def small_x(rng, M):
+    """bf16-exact small values (k/8, |k| <= 32) so every sum is exact in fp64."""
+    return rng.integers(-32, 33, size=(M, 128)).astype(np.float64) / 8.0
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 16])
+def test_bf16_fragments_match_dense(M):
+    rng = np.random.default_rng(M)
+    Wv = rng.integers(-64, 65, size=(16, 128)).astype(np.float32) / 16.0      # bf16-exact
+    wb = O.f32_to_bf16_bits(Wv)
+    wbytes = [wb[n].astype("<u2").tobytes() for n in range(16)]
+    wbytes = [np.frombuffer(b, dtype=np.uint8) for b in wbytes]
+    x = small_x(rng, M)
+    assert np.array_equal(emulate_tile("bf16", wbytes, x), x @ Wv.astype(np.float64).T)
+
+
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_fp8_fragments_match_dense(M):
+    rng = np.random.default_rng(10 + M)
+    tab = O.e4m3_table()
+    codes = rng.integers(0, 256, size=(16, 128)).astype(np.uint8)
+    codes[np.isnan(tab[codes])] = 0x38                                         # no NaN codes (value 1.0)
+    x = small_x(rng, M)
+    ref = x @ tab[codes].astype(np.float64).T
+    assert np.array_equal(emulate_tile("fp8", list(codes), x), ref)
+
+
+@pytest.mark.parametrize("fmt,M", [("int4", 1), ("int4", 4), ("int4zp", 2), ("int4zp", 16)])
+def test_int4_fragments_and_group_term_match_dense(fmt, M):
+    rng = np.random.default_rng(20 + M)
+    q = rng.integers(0, 16, size=(16, 128)).astype(np.uint8)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)                # byte j = weights 2j (lo), 2j+1 (hi)
+    z = np.full(16, 8) if fmt == "int4" else rng.integers(0, 16, size=16)
+    s = rng.integers(1, 5, size=16).astype(np.float64) / 4.0
+    x = small_x(rng, M)
+    deq = (q.astype(np.float64) - z[:, None]) * s[:, None]
+    got = emulate_tile(fmt, list(packed), x, zc=128.0 + z, s=s)
+    assert np.array_equal(got, x @ deq.T)
+
+
+def test_int4_decode_constant_is_bf16_128():
+    assert O.bf16_bits_to_f32(np.array([C43 & 0xFFFF], dtype=np.uint16))[0] == 195.0   # 0x4343; 0x4300 = 128
+    assert O.bf16_bits_to_f32(np.array([0x4300 | 15], dtype=np.uint16))[0] == 143.0
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# work decomposition
+# ---------------------------------------------------------------------------------------------------------------
+def plan(fmt, M, N, K, P, U, W, S):
+    """gemv_batch.h batch_plan + launch_batch (None when no chunk of U k-blocks fits)."""
+    i4 = fmt in ("int4", "int4zp")
+    KB = -(-K // 128)
+    kbs = -(-KB // S)
+    per_kb = S * M * 256 + (S * 64 if i4 else 0)
+    fixed = S * M * 16
+    if fixed + per_kb * U > LDS:
+        return None
+    C = (LDS - fixed) // per_kb
+    C -= C % U
+    C = min(C, -(-kbs // U) * U)
+    xrow = C * 256 + 16
+    xb = fixed + per_kb * C
+    pb = (W // S) * (S - 1) * P * 1024 if S > 1 else 0
+    ntiles = -(-N // 16)
+    return dict(KB=KB, kbs=kbs, C=C, nchunks=-(-kbs // C), xrow=xrow, xs_off=S * M * xrow, lds=max(xb, pb),
+                ntiles=ntiles, grid=-(-ntiles // ((W // S) * P)))
+
+
+def replay(fmt, M, N, K, P, U, W, S):
+    p = plan(fmt, M, N, K, P, U, W, S)
+    assert p is not None
+    i4 = fmt in ("int4", "int4zp")
+    seen = np.zeros((p["ntiles"], p["KB"]), dtype=np.int64)
+    C, kbs = p["C"], p["kbs"]
+    assert C % U == 0 and C >= U
+    # staging: vector q of chunk c -> (split, row, kbl, v); LDS addresses inside the x region
+    nvec = S * M * C * 16
+    assert (nvec - 1) // 16 // C // M < S
+    last = ((S - 1) * M + (M - 1)) * p["xrow"] + (C - 1) * 256 + 15 * 16 + 16
+    assert last <= p["xs_off"] <= p["lds"]
+    if i4:
+        assert p["xs_off"] + S * C * 16 * 4 <= p["lds"]
+    for b in range(p["grid"]):
+        slots = set()
+        for w in range(W):
+            split, tile0 = w % S, (b * (W // S) + w // S) * P
+            kb0 = split * kbs
+            nkb = max(0, min(p["KB"], kb0 + kbs) - kb0)
+            for c in range(p["nchunks"]):
+                t_end = nkb - c * C
+                for kbl0 in range(0, C, U):
+                    if kbl0 >= t_end:
+                        break
+                    for u in range(U):
+                        kbl, t = kbl0 + u, c * C + kbl0 + u
+                        if kbl < t_end:
+                            kb = kb0 + t
+                            # the chunk slot read holds k-block split*kbs + c*C + kbl of this split
+                            assert split * kbs + c * C + kbl == kb and kb < p["KB"]
+                            # A-fragment reads stay in the split's rows of this chunk
+                            assert (split * M + M - 1) * p["xrow"] + kbl * 256 + 256 <= p["xs_off"]
+                            for tt in range(P):
+                                if tile0 + tt < p["ntiles"]:
+                                    seen[tile0 + tt, kb] += 1
+            if S > 1 and split > 0:
+                for tt in range(P):
+                    slot = ((w // S) * (S - 1) + split - 1) * P + tt
+                    assert slot not in slots
+                    slots.add(slot)
+                    assert (slot + 1) * 1024 <= p["lds"]
+    assert (seen == 1).all(), f"coverage: min {seen.min()} max {seen.max()}"
+    return p
+
+
+TABLE = {
+    "bf16": [(1, 2), (1, 4), (2, 2)],
+    "fp8": [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4), (4, 2)],
+    "int4": [(1, 4), (1, 8), (2, 2), (2, 4), (2, 8), (4, 2), (4, 4)],
+}
+TABLE["int4zp"] = TABLE["int4"]
+WS = [(4, 1), (4, 2), (4, 4), (8, 1), (8, 2), (8, 4), (8, 8)]
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4"])
+def test_every_tile_and_k_block_once(fmt):
+    kmult = {"bf16": 8, "fp8": 16}.get(fmt, 128)
+    shapes = [(1, 16 * 1 + 3, 128), (3, 100, 3 * 128), (2, 257, 1000 // kmult * kmult), (16, 64, 4096),
+              (16, 40, 14336), (7, 4608, 3584), (5, 33, 18944)]
+    n = 0
+    for (M, N, K), (P, U), (W, S) in itertools.product(shapes, TABLE[fmt], WS):
+        if K % kmult or plan(fmt, M, N, K, P, U, W, S) is None:
+            continue
+        replay(fmt, M, N, K, P, U, W, S)
+        n += 1
+    assert n > 50
+
+
+def test_table_matches_library(gemv_lib):
+    """The variant tables replayed here are the library's, and the library's default pick always has a plan."""
+    L = gemv_lib
+    for fmt, k in KINDS.items():
+        got = {(v["P"], v["U"], v["W"], v["S"]) for v in L.variants_batch[fmt]}
+        want = {(P, U, W, S) for (P, U), (W, S) in itertools.product(TABLE[fmt], WS)}
+        assert got == want, fmt
+        for M in (1, 2, 4, 8, 16):
+            for N, K in [(4096, 4096), (28672, 4096), (4096, 14336), (4608, 3584), (3584, 18944), (128256, 4096)]:
+                v = L.batch_pick_variant(fmt, M, N, K)
+                assert 0 <= v < len(L.variants_batch[fmt])
+                d = L.variants_batch[fmt][v]
+                assert plan(fmt, M, N, K, d["P"], d["U"], d["W"], d["S"]) is not None
+        assert L.batch_pick_variant(fmt, 17, 4096, 4096) == -1
+        assert L.batch_pick_variant(fmt, 0, 4096, 4096) == -1
