@@ -14,9 +14,14 @@
 //     k-block, so each load instruction reads 64 contiguous bytes of 16 rows.
 //   * Dequantisation in registers as in the M = 1 kernel: FP8 by the gfx950 e4m3 -> f32 convert packed to bf16 (exact),
 //     INT4 by v_perm of the nibbles under a 0x43 byte, giving bf16 (128 + q) exactly; the INT4 group term
-//     (128 + z) * sum_k x[m,k] is removed per group with fp32 x sums computed while x is staged.
-//   * x is staged in LDS per K-chunk (all of K when M*K fits, as at M = 1), in the column order each format's MFMA
-//     steps take (INT4: (k, k+2, k+4, k+6, k+1, k+3, k+5, k+7) within each 8, matching the nibble decode).
+//     (128 + z) * sum_k x[m,k] is removed per group, with the group sums of x taken by one more MFMA chain against a
+//     B operand of ones (it lands in the lanes and rows of D that need it, shared by the wave's P tiles).
+//   * x (the A operand) comes one of two ways (knob X):
+//       X=0: staged in LDS per K-chunk (all of K when M*K fits, as at M = 1) in the column order the format's MFMA
+//            steps take (INT4: (k, k+2, k+4, k+6, k+1, k+3, k+5, k+7) within each 8, matching the nibble decode);
+//            a chunk change costs two block barriers and drains the load pipeline.
+//       X=1: loaded per k-block straight into registers with the weights (L2-resident: x is at most 16 rows), in the
+//            same pipeline; no LDS, no barrier, no K limit -- the choice for many rows or long K.
 //   * Each wave owns P tiles and one of S K-splits; the S waves sharing a tile combine their fp32 partials through
 //     LDS in split order after a block barrier, so results are bitwise reproducible. U k-blocks of loads are in flight
 //     per wave; the loads of the next k-blocks are issued before the current ones are consumed.
@@ -37,6 +42,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kTileRows = 16;    // weight rows per MFMA tile
 constexpr int kBlockCols = 128;  // columns per k-block (4 MFMA steps of 32; one INT4 group)
 constexpr int kMaxBatch = 16;    // activation rows per call
+
+// Cache policy of the weight loads (buffer-load aux bits). 0, the default policy: measured on MI355X ~10% faster
+// than nt (2) for this kernel's 64-byte-per-row load pattern (FP8 gate_up 28672x4096: 22.1 vs 24.5 us at M = 1).
+#ifndef PAIA_BATCH_WAUX
+#define PAIA_BATCH_WAUX 0
+#endif
 
 template <int F>
 struct BatchFmt {
@@ -62,8 +73,7 @@ struct BatchParams {
     int kbs;                // k-blocks per split: ceil(KB / S)
     int C;                  // k-blocks per LDS chunk of each split (a multiple of U)
     int nchunks;            // ceil(kbs / C)
-    uint32_t xrow;          // LDS bytes per staged x row: C*256 + 16 (the 16 spreads rows over the banks)
-    uint32_t xs_off;        // LDS offset of the INT4 x group sums [S][C][16] fp32
+    uint32_t xrow;          // X=0: LDS bytes per staged x row: C*256 + 16 (the 16 spreads rows over the banks)
 };
 
 // First column (within a k-block) of the 8 that MFMA step j takes from lane group h; the other steps' columns follow
@@ -74,18 +84,24 @@ __host__ __device__ constexpr int step_col(int j, int h)
     return F == kBF16 ? 32 * j + 8 * h : (F == kFP8 ? 64 * (j >> 1) + 16 * h + 8 * (j & 1) : 32 * h + 8 * j);
 }
 
-// LDS layout of a launch: x chunk [S][M][xrow] (+ INT4 sums), reused for the split-K partials after the last chunk.
-template <int F>
+// LDS layout of a launch: X=0 x chunk [S][M][xrow], reused for the split-K partials after the last chunk.
 __host__ __device__ constexpr uint32_t batch_x_bytes(int S, int M, int C)
 {
-    return (uint32_t)(S * M) * (uint32_t)(C * 256 + 16) + ((F == kI4 || F == kI4ZP) ? (uint32_t)(S * C * 64) : 0u);
+    return (uint32_t)(S * M) * (uint32_t)(C * 256 + 16);
 }
 __host__ __device__ constexpr uint32_t batch_part_bytes(int S, int W, int P)
 {
     return S > 1 ? (uint32_t)((W / S) * (S - 1) * P) * 1024u : 0u;
 }
 
-template <int F, int P, int U, int W>
+// INT4 x vector (x0..x7 as bf16 pairs) re-paired to the nibble decode order (x0,x2),(x4,x6),(x1,x3),(x5,x7).
+__device__ __forceinline__ u32x4 i4_pair_x(const u32x4 a)
+{
+    return u32x4{__builtin_amdgcn_perm(a.y, a.x, 0x05040100u), __builtin_amdgcn_perm(a.w, a.z, 0x05040100u),
+                 __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), __builtin_amdgcn_perm(a.w, a.z, 0x07060302u)};
+}
+
+template <int F, int P, int U, int W, int XM>
 __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
 {
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
@@ -105,14 +121,16 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
     const int M = p.M;
     const uint32_t c43 = (uint32_t)__builtin_amdgcn_readfirstlane(0x43434343);
 
-    // Per-tile descriptors bounded to the tile's rows: rows >= N read zeros with no traffic.
+    // Per-tile descriptors bounded to the tile's rows: rows >= N read zeros with no traffic. The row count goes
+    // through readfirstlane: computed with v_med3 it would sit in a VGPR, and a descriptor built from a VGPR makes
+    // the compiler wrap every load in a waterfall loop.
     __amdgpu_buffer_rsrc_t rw[P];
     __amdgpu_buffer_rsrc_t rm[I4 ? P : 1];
     __amdgpu_buffer_rsrc_t rz[F == kI4ZP ? P : 1];
 #pragma unroll
     for (int t = 0; t < P; ++t) {
         const int row0 = (tile0 + t) * kTileRows;
-        const uint32_t rows = (uint32_t)max(0, min(kTileRows, p.N - row0));
+        const uint32_t rows = (uint32_t)__builtin_amdgcn_readfirstlane(max(0, min(kTileRows, p.N - row0)));
         const size_t r0 = rows ? (size_t)row0 : 0;
         rw[t] = make_rsrc(p.W + r0 * p.row_bytes, rows * p.row_bytes);
         if constexpr (I4) rm[t] = make_rsrc((const uint8_t*)p.meta + r0 * p.meta_bytes, rows * p.meta_bytes);
@@ -129,10 +147,16 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
     const uint32_t lmeta = (uint32_t)ln * p.meta_bytes;
     const uint32_t lzero = (uint32_t)ln * p.zbytes;
 
+    // X=1: A-fragment offsets of this lane (row ln of x; rows >= M read zeros), step j adds a constant.
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
+    const bool xrow_ok = ln < M;
+    const uint32_t lxa = ((uint32_t)ln * (uint32_t)p.K + (uint32_t)step_col<F>(0, lh)) * 2u;
+
     struct Stage {
         u32x4 w[P][L];
         uint32_t s[I4 ? P : 1];
         uint32_t z[F == kI4ZP ? P : 1];
+        u32x4 a[XM ? 4 : 1];
     };
     // Loads of this wave's k-block number t (t >= nkb: out of range, zeros, no traffic). Unconditional, so the
     // compiler never has to wait for the other stages' loads.
@@ -145,7 +169,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
             uint32_t off = base + (uint32_t)(64 * i);
             if constexpr (!I4) off = kb * kBlockCols < klim[i] ? off : kOOB;
 #pragma unroll
-            for (int tt = 0; tt < P; ++tt) B.w[tt][i] = ld16<2>(rw[tt], off, 0u);
+            for (int tt = 0; tt < P; ++tt) B.w[tt][i] = ld16<PAIA_BATCH_WAUX>(rw[tt], off, 0u);
         }
         if constexpr (I4) {
             const uint32_t moff = ok ? lmeta + (uint32_t)kb * 2u : kOOB;
@@ -154,6 +178,15 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
             for (int tt = 0; tt < P; ++tt) {
                 B.s[tt] = ld_u16(rm[tt], moff, 0u);
                 if constexpr (F == kI4ZP) B.z[tt] = ld_u8(rz[tt], zoff, 0u);
+            }
+        }
+        if constexpr (XM) {
+            const uint32_t xb = ok && xrow_ok ? lxa + (uint32_t)kb * 256u : kOOB;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t off = xb + (uint32_t)(2 * (step_col<F>(j, lh) - step_col<F>(0, lh)));
+                if constexpr (!I4) off = kb * kBlockCols + step_col<F>(j, lh) < p.K ? off : kOOB;
+                B.a[j] = ld16<0>(xrs, off, 0u);
             }
         }
     };
@@ -172,11 +205,9 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
         }
     };
 
-    // ---- x staging: chunk c holds, for every split s, k-blocks s*kbs + c*C .. +C-1 of all M rows. A staged vector is
-    // 8 columns (16 bytes); the 16 vectors of a k-block row are 16 consecutive threads, i.e. one DPP row, which sums
-    // them for the INT4 group term.
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
-    const int nvec = S * M * p.C * 16;
+    // ---- X=0 x staging: chunk c holds, for every split s, k-blocks s*kbs + c*C .. +C-1 of all M rows, one 16-byte
+    // vector (8 columns) per thread and step.
+    const int nvec = XM ? 0 : S * M * p.C * 16;
     auto x_src = [&](int c, int q) -> uint32_t {
         const int v = q & 15;
         int r = q >> 4;
@@ -194,31 +225,18 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
         const int kbl = r % p.C;
         r /= p.C;
         const int m = r % M, s2 = r / M;
-        if constexpr (I4) {
-            float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
-                        (bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16))) +
-                       ((bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16)) +
-                        (bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16)));
-            s8 = dpp_add<0xB1, 0xF>(s8);    // quad_perm [1,0,3,2]
-            s8 = dpp_add<0x4E, 0xF>(s8);    // quad_perm [2,3,0,1]
-            s8 = dpp_add<0x124, 0xF>(s8);   // row_ror:4
-            s8 = dpp_add<0x128, 0xF>(s8);   // row_ror:8 -> the k-block's sum in every lane of the row
-            if (vi == 0) reinterpret_cast<float*>(smem + p.xs_off)[(s2 * p.C + kbl) * 16 + m] = s8;
-            const u32x4 a = v;
-            v.x = (a.x & 0xFFFFu) | (a.y << 16);
-            v.y = (a.z & 0xFFFFu) | (a.w << 16);
-            v.z = (a.x >> 16) | (a.y & 0xFFFF0000u);
-            v.w = (a.z >> 16) | (a.w & 0xFFFF0000u);
-        }
+        if constexpr (I4) v = i4_pair_x(v);
         *reinterpret_cast<u32x4*>(smem + (uint32_t)(s2 * M + m) * p.xrow + (uint32_t)(kbl * 256 + vi * 16)) = v;
     };
     auto stage_x = [&](int c) {
         for (int q = (int)threadIdx.x; q < nvec; q += W * kWave) x_put(q, ld16<0>(xrs, x_src(c, q), 0u));
     };
 
-    // A fragments and INT4 sums: lane reads row (ln < M ? ln : 0) of its split's chunk.
-    const uint32_t lx = (uint32_t)(split * M + (ln < M ? ln : 0)) * p.xrow + (uint32_t)(2 * step_col<F>(0, lh));
-    const uint32_t lxs = p.xs_off + (uint32_t)(split * p.C * 16 + 4 * lh) * 4u;
+    // X=0 A fragments: lane reads row (ln < M ? ln : 0) of its split's chunk.
+    const uint32_t lx = XM ? 0u : (uint32_t)(split * M + (ln < M ? ln : 0)) * p.xrow + (uint32_t)(2 * step_col<F>(0, lh));
+    // bf16 1.0 pairs: the B operand that turns an MFMA into row sums of A
+    const uint32_t one2 = (uint32_t)__builtin_amdgcn_readfirstlane(0x3F803F80);
+    const u32x4 ones = {one2, one2, one2, one2};
 
     f32x4 acc[P];
 #pragma unroll
@@ -228,11 +246,20 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
     auto consume = [&](const Stage& B, int kbl, int t_idx) {
         bf16x8 a[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            a[j] = *reinterpret_cast<const bf16x8*>(smem + lx + (uint32_t)kbl * 256u +
-                                                    (uint32_t)(2 * (step_col<F>(j, lh) - step_col<F>(0, lh))));
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (XM)
+                a[j] = __builtin_bit_cast(bf16x8, I4 ? i4_pair_x(B.a[j]) : B.a[j]);
+            else
+                a[j] = *reinterpret_cast<const bf16x8*>(smem + lx + (uint32_t)kbl * 256u +
+                                                        (uint32_t)(2 * (step_col<F>(j, lh) - step_col<F>(0, lh))));
+        }
+        // INT4: group sums of x for the D rows this lane holds (rows 4*lh + v), from an MFMA chain against ones
         f32x4 xs4 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (I4) xs4 = *reinterpret_cast<const f32x4*>(smem + lxs + (uint32_t)kbl * 64u);
+        if constexpr (I4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xs4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, ones), xs4, 0, 0, 0);
+        }
 #pragma unroll
         for (int t = 0; t < P; ++t) {
             if constexpr (F == kBF16) {
@@ -276,33 +303,31 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
         }
     };
 
-    // INT4 sums of the never-staged rows m >= M: zero once (written by no one else).
-    if constexpr (I4) {
-        float* xsum = reinterpret_cast<float*>(smem + p.xs_off);
-        for (int i = (int)threadIdx.x; i < S * p.C * 16; i += W * kWave)
-            if ((i & 15) >= M) xsum[i] = 0.0f;
-    }
-
-    // First chunk: x loads go out first, then the first U k-blocks of weights, then x is stored (waiting on the x
-    // loads only) while the weights are in flight.
-    constexpr int XE = 2;
+    // First chunk (X=0): x loads go out first, then the first U k-blocks of weights, then x is stored (waiting on the
+    // x loads only) while the weights are in flight. X=1 only issues the first U k-blocks.
+    constexpr int XE = XM ? 1 : 2;
     u32x4 xe[XE];
+    if constexpr (!XM) {
 #pragma unroll
-    for (int e = 0; e < XE; ++e) {
-        const int q = (int)threadIdx.x + e * W * kWave;
-        xe[e] = ld16<0>(xrs, q < nvec ? x_src(0, q) : kOOB, 0u);
+        for (int e = 0; e < XE; ++e) {
+            const int q = (int)threadIdx.x + e * W * kWave;
+            xe[e] = ld16<0>(xrs, q < nvec ? x_src(0, q) : kOOB, 0u);
+        }
     }
     Stage buf[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) issue(buf[u], u);
     ep_load();
+    if constexpr (!XM) {
 #pragma unroll
-    for (int e = 0; e < XE; ++e) {
-        const int q = (int)threadIdx.x + e * W * kWave;
-        if (q < nvec) x_put(q, xe[e]);
+        for (int e = 0; e < XE; ++e) {
+            const int q = (int)threadIdx.x + e * W * kWave;
+            if (q < nvec) x_put(q, xe[e]);
+        }
+        for (int q = (int)threadIdx.x + XE * W * kWave; q < nvec; q += W * kWave)
+            x_put(q, ld16<0>(xrs, x_src(0, q), 0u));
+        __syncthreads();
     }
-    for (int q = (int)threadIdx.x + XE * W * kWave; q < nvec; q += W * kWave) x_put(q, ld16<0>(xrs, x_src(0, q), 0u));
-    __syncthreads();
 
     for (int c = 0; c < p.nchunks; ++c) {
         if (c > 0) {
@@ -364,43 +389,51 @@ constexpr uint32_t kBatchLds = 65536;
 
 // Fill in the launch plan (k-blocks, splits, chunking, LDS). Returns the LDS bytes, or 0 if no chunk of U k-blocks
 // fits (too many activation rows x splits for this U).
-template <int F, int P, int U, int W>
-uint32_t batch_plan(BatchParams& p)
+// Fill in the launch plan (k-blocks, splits, chunking, LDS). Returns the LDS bytes (possibly 0 for X=1 without
+// split-K), or -1 if no chunk of U k-blocks fits (X=0: too many activation rows x splits for this U).
+template <int P, int U, int W, int XM>
+int64_t batch_plan(BatchParams& p)
 {
     p.KB = (p.K + kBlockCols - 1) / kBlockCols;
     p.ntiles = (p.N + kTileRows - 1) / kTileRows;
     p.kbs = (p.KB + p.S - 1) / p.S;
-    const uint32_t per_kb = batch_x_bytes<F>(p.S, p.M, 1) - batch_x_bytes<F>(p.S, p.M, 0);
-    const uint32_t fixed = batch_x_bytes<F>(p.S, p.M, 0);
-    if (fixed + per_kb * U > kBatchLds) return 0;
+    const int cap = (p.kbs + U - 1) / U * U;
+    const uint32_t pb = batch_part_bytes(p.S, W, P);
+    if (XM) {
+        p.C = cap;
+        p.nchunks = 1;
+        p.xrow = 0;
+        return pb;
+    }
+    const uint32_t per_kb = batch_x_bytes(p.S, p.M, 1) - batch_x_bytes(p.S, p.M, 0);
+    const uint32_t fixed = batch_x_bytes(p.S, p.M, 0);
+    if (fixed + per_kb * U > kBatchLds) return -1;
     int C = (int)((kBatchLds - fixed) / per_kb);
     C -= C % U;
-    const int cap = (p.kbs + U - 1) / U * U;
     if (C > cap) C = cap;
     p.C = C;
     p.nchunks = (p.kbs + C - 1) / C;
     p.xrow = (uint32_t)(C * 256 + 16);
-    p.xs_off = (uint32_t)(p.S * p.M) * p.xrow;
-    const uint32_t xb = batch_x_bytes<F>(p.S, p.M, C), pb = batch_part_bytes(p.S, W, P);
+    const uint32_t xb = batch_x_bytes(p.S, p.M, C);
     return xb > pb ? xb : pb;
 }
 
 // Launch on `st`. Arguments were validated by the caller (1 <= M <= 16, S divides W). Returns 0, -2 or a hipError_t.
-template <int F, int P, int U, int W>
+template <int F, int P, int U, int W, int XM>
 int launch_batch(BatchParams p, hipStream_t st)
 {
-    const uint32_t lds = batch_plan<F, P, U, W>(p);
-    if (lds == 0) return -2;
+    const int64_t lds = batch_plan<P, U, W, XM>(p);
+    if (lds < 0) return -2;
     const int tiles_per_block = (W / p.S) * P;
     const int grid = (p.ntiles + tiles_per_block - 1) / tiles_per_block;
-    hipLaunchKernelGGL((gemv_batch_kernel<F, P, U, W>), dim3(grid), dim3(W * kWave), lds, st, p);
+    hipLaunchKernelGGL((gemv_batch_kernel<F, P, U, W, XM>), dim3(grid), dim3(W * kWave), (uint32_t)lds, st, p);
     return (int)hipGetLastError();
 }
 
 using BatchLaunchFn = int (*)(BatchParams, hipStream_t);
 
 struct BatchVariant {
-    int P, U, W, S;
+    int P, U, W, S, X;
     BatchLaunchFn fn;
 };
 

@@ -7,7 +7,8 @@
 // synchronisation. x is bf16 [M][K] and y bf16 [M][N], both row-major.
 //
 // Variant knobs: P tiles of 16 rows per wave, U k-blocks (128 columns) of loads in flight per wave, W waves per block,
-// S waves sharing a tile along K (split-K inside the block). variant < 0 selects paia_gemv_batch_pick_variant's.
+// S waves sharing a tile along K (split-K inside the block), X how x reaches the matrix cores (0 staged in LDS per
+// K-chunk, 1 loaded with the weights). variant < 0 selects paia_gemv_batch_pick_variant's.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -17,15 +18,16 @@
 namespace {
 using namespace paia;
 
-template <int F, int P, int U, int W>
+template <int F, int P, int U, int W, int X>
 int launch_b(BatchParams p, hipStream_t st)
 {
-    return launch_batch<F, P, U, W>(p, st);
+    return launch_batch<F, P, U, W, X>(p, st);
 }
 
-#define BV(F, P, U, W, S) {P, U, W, S, &launch_b<F, P, U, W>},
-#define BV_W(F, P, U) BV(F, P, U, 4, 1) BV(F, P, U, 4, 2) BV(F, P, U, 4, 4) \
-                      BV(F, P, U, 8, 1) BV(F, P, U, 8, 2) BV(F, P, U, 8, 4) BV(F, P, U, 8, 8)
+#define BV(F, P, U, W, S, X) {P, U, W, S, X, &launch_b<F, P, U, W, X>},
+#define BV_S(F, P, U, X) BV(F, P, U, 4, 1, X) BV(F, P, U, 4, 2, X) BV(F, P, U, 4, 4, X) \
+                         BV(F, P, U, 8, 1, X) BV(F, P, U, 8, 2, X) BV(F, P, U, 8, 4, X) BV(F, P, U, 8, 8, X)
+#define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1)
 // register budget: P * U * (16-byte loads per k-block) <= 16 buffers of 4 VGPRs
 const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2)};
 const BatchVariant kFp8Batch[] = {BV_W(kFP8, 1, 2) BV_W(kFP8, 1, 4) BV_W(kFP8, 1, 8) BV_W(kFP8, 2, 2)
@@ -35,6 +37,7 @@ const BatchVariant kI4Batch[] = {BV_W(kI4, 1, 4) BV_W(kI4, 1, 8) BV_W(kI4, 2, 2)
 const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4ZP, 2, 2) BV_W(kI4ZP, 2, 4)
                                        BV_W(kI4ZP, 2, 8) BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4)};
 #undef BV
+#undef BV_S
 #undef BV_W
 
 struct Table {
@@ -52,59 +55,41 @@ Table table(int kind)
     }
 }
 
-int find(const Table& t, int P, int U, int W, int S)
+int find(const Table& t, int P, int U, int W, int S, int X)
 {
     for (int i = 0; i < t.n; ++i)
-        if (t.v[i].P == P && t.v[i].U == U && t.v[i].W == W && t.v[i].S == S) return i;
+        if (t.v[i].P == P && t.v[i].U == U && t.v[i].W == W && t.v[i].S == S && t.v[i].X == X) return i;
     return -1;
 }
 
-// LDS bytes a variant needs for this shape (0 if no chunk fits), computed like batch_plan.
-uint32_t plan_lds(int kind, int M, int K, int P, int U, int W, int S)
+// Whether variant v can run (M, K): X=0 needs a chunk of U k-blocks of x for all S splits in LDS.
+bool fits(const BatchVariant& v, int M)
 {
-    const int KB = (K + kBlockCols - 1) / kBlockCols;
-    const int kbs = (KB + S - 1) / S;
-    const bool i4 = kind >= 2;
-    const uint32_t per_kb = (uint32_t)(S * M) * 256u + (i4 ? (uint32_t)S * 64u : 0u);
-    const uint32_t fixed = (uint32_t)(S * M) * 16u;
-    if (fixed + per_kb * (uint32_t)U > kBatchLds) return 0;
-    int C = (int)((kBatchLds - fixed) / per_kb);
-    C -= C % U;
-    const int cap = (kbs + U - 1) / U * U;
-    if (C > cap) C = cap;
-    const uint32_t xb = fixed + per_kb * (uint32_t)C;
-    const uint32_t pb = S > 1 ? (uint32_t)((W / S) * (S - 1) * P) * 1024u : 0u;
-    return xb > pb ? xb : pb;
+    return v.X == 1 || batch_x_bytes(v.S, M, v.U) <= kBatchLds;
 }
 
-// Default choice: the format's tile/pipeline shape, then the fewest K-splits that put at least ~8 waves on every CU
-// (at least 4 k-blocks per split, and the x chunk must fit).
+// Default choice, fitted to MI355X sweeps of the Llama/Qwen projection shapes at M = 1, 4, 16 (FP8 and INT4):
+//   * split-K S: the fewest splits (<= 8, >= 2 k-blocks each) that give >= 3072 waves (12 per CU);
+//   * x in LDS (X=0) unless the splits x rows make staging cost more than it saves (M*S >= 32 with S >= 4: each block
+//     would stage half or more of its weight bytes again as x) or not even one chunk of U k-blocks fits;
+//   * one tile per wave; two when x comes with the weights and M >= 4, so the two tiles share each x load.
 int pick(int kind, int M, int N, int K)
 {
     const Table t = table(kind);
     if (!t.v || M < 1 || M > kMaxBatch || N <= 0 || K <= 0) return -1;
-    int P = 2, U = 4, W = 4;
-    if (kind == 0) {
-        P = 1;
-        U = 4;
-    }
+    const int W = 8;
     const int ntiles = (N + kTileRows - 1) / kTileRows;
     const int KB = (K + kBlockCols - 1) / kBlockCols;
-    const DeviceFacts df = device_facts();
-    const int want = (df.cus > 0 ? df.cus : 256) * 8;
-    int best = -1;
-    for (int S = 1; S <= 4; S *= 2) {
-        if (S > 1 && (KB + S - 1) / S < 4) break;
-        if (plan_lds(kind, M, K, P, U, W, S) == 0) break;
-        best = find(t, P, U, W, S);
-        if ((ntiles + P - 1) / P * S >= want) break;
+    int S = 1;
+    while (S < W && ntiles * S < 3072 && (KB + 2 * S - 1) / (2 * S) >= 2) S *= 2;
+    int P = 1, U = kind >= 2 ? 4 : 2;
+    int X = 0;
+    if ((M * S >= 32 && S >= 4) || batch_x_bytes(S, M, U) > kBatchLds) X = 1;
+    if (X == 1 && M >= 4) {
+        P = 2;
+        U = kind >= 2 ? 4 : 2;
     }
-    if (best < 0) {
-        // large M x K: the smallest pipeline that fits
-        for (int i = 0; i < t.n && best < 0; ++i)
-            if (t.v[i].S == 1 && plan_lds(kind, M, K, t.v[i].P, t.v[i].U, t.v[i].W, 1) != 0) best = i;
-    }
-    return best;
+    return find(t, P, U, W, S, X);
 }
 
 int batch_impl(int kind, BatchParams p, int variant, void* stream)
@@ -112,6 +97,7 @@ int batch_impl(int kind, BatchParams p, int variant, void* stream)
     const Table t = table(kind);
     if (variant < 0) variant = pick(kind, p.M, p.N, p.K);
     if (variant < 0 || variant >= t.n) return -1;
+    if (!fits(t.v[variant], p.M)) return -2;
     p.S = t.v[variant].S;
     return t.v[variant].fn(p, static_cast<hipStream_t>(stream));
 }
@@ -130,7 +116,7 @@ extern "C" {
 
 int paia_gemv_batch_variant_count(int kind) { return table(kind).n; }
 
-int paia_gemv_batch_variant_info(int kind, int v, int* P, int* U, int* W, int* S)
+int paia_gemv_batch_variant_info(int kind, int v, int* P, int* U, int* W, int* S, int* X)
 {
     const Table t = table(kind);
     if (v < 0 || v >= t.n) return -1;
@@ -138,6 +124,7 @@ int paia_gemv_batch_variant_info(int kind, int v, int* P, int* U, int* W, int* S
     *U = t.v[v].U;
     *W = t.v[v].W;
     *S = t.v[v].S;
+    *X = t.v[v].X;
     return 0;
 }
 

@@ -22,11 +22,20 @@ def kind_of(fmt: str) -> str:
 
 
 class GemvCase:
+    """mode: 'fused' (the M = 1 kernels), 'naive' / 'unfused' (INT4 controls), or 'batch' (the small-batch matrix-core
+    kernels, M = 1..16 activation rows; `variant` then indexes lib.variants_batch[fmt])."""
+
     def __init__(self, lib, fmt: str, N: int, K: int, bias: bool = False, variant: int | None = None,
-                 mode: str = "fused", name: str | None = None):
-        self.lib, self.fmt, self.N, self.K, self.bias, self.mode = lib, fmt, N, K, bias, mode
-        self.name = name or f"{fmt}_{N}x{K}"
-        self.variant = lib.pick_variant(fmt, N, K) if variant is None else int(variant)
+                 mode: str = "fused", name: str | None = None, M: int = 1):
+        self.lib, self.fmt, self.N, self.K, self.bias, self.mode, self.M = lib, fmt, N, K, bias, mode, M
+        assert M == 1 or mode == "batch", "M > 1 runs the batch kernels"
+        self.name = name or (f"{fmt}_{N}x{K}" if mode != "batch" else f"{fmt}_M{M}_{N}x{K}")
+        if variant is not None:
+            self.variant = int(variant)
+        elif mode == "batch":
+            self.variant = lib.batch_pick_variant(fmt, M, N, K)
+        else:
+            self.variant = lib.pick_variant(fmt, N, K)
         self.copies: list = []
         self.ptrs: list = []
         self.scratch = None
@@ -34,7 +43,7 @@ class GemvCase:
 
     # ---- accounting --------------------------------------------------------------------------------------
     def bytes(self) -> dict:
-        return gemv_bytes(self.fmt, self.N, self.K, self.bias)
+        return gemv_bytes(self.fmt, self.N, self.K, self.bias, self.M)
 
     def footprint(self) -> int:
         return self.bytes()["total"]
@@ -54,17 +63,27 @@ class GemvCase:
             c["Wq"] = torch.randint(0, 256, (N, K // 2), device=dev, generator=g, dtype=torch.uint8)
             c["scales"] = (0.001 + 0.009 * torch.rand(N, G, device=dev, generator=g)).to(torch.bfloat16)
             c["zeros"] = quant.pack_zeros(torch.randint(0, 16, (N, G), device=dev, generator=g, dtype=torch.uint8))
-        c["x"] = torch.randn(K, device=dev, generator=g).to(torch.bfloat16)
+        c["x"] = torch.randn(*self._xshape(), device=dev, generator=g).to(torch.bfloat16)
         c["bias"] = (0.02 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16) if self.bias else None
         return c
+
+    def _xshape(self):
+        return (self.M, self.K) if self.mode == "batch" else (self.K,)
 
     def build(self, n_copies: int, device="cuda", seed: int = 1234):
         dev = torch.device(device)
         self.ops0 = make_operands(self.fmt, self.N, self.K, bias=self.bias)
+        if self.mode == "batch":
+            # M activation rows: row 0 is the seeded x of make_operands, the others seeded after it
+            gx = torch.Generator().manual_seed(2000 + self.M + self.N + self.K)
+            xs = torch.randn(self.M, self.K, generator=gx).to(torch.bfloat16)
+            xs[0] = self.ops0["x"]
+            self.ops0["x"] = xs
         g = torch.Generator(device=dev).manual_seed(seed)
         self.copies = [to_device(self.ops0, dev)] + [self._random_copy(dev, g) for _ in range(n_copies - 1)]
+        yshape = (self.M, self.N) if self.mode == "batch" else (self.N,)
         for c in self.copies:
-            c["y"] = torch.empty(self.N, dtype=torch.bfloat16, device=dev)
+            c["y"] = torch.empty(*yshape, dtype=torch.bfloat16, device=dev)
         if self.mode == "unfused":
             self.scratch = torch.empty(self.N * self.K, dtype=torch.bfloat16, device=dev)
         self.ptrs = [self._ptrs(c) for c in self.copies]
@@ -88,6 +107,21 @@ class GemvCase:
     def call(self, i: int, stream=None):
         L, N, K, v = self.lib, self.N, self.K, self.variant
         P = self.ptrs[i]
+        if self.mode == "batch":
+            M = self.M
+            if self.fmt == "bf16":
+                W, x, b, y = P
+                L.batch_bf16(W, x, b, y, M, N, K, v, stream)
+            elif self.fmt == "fp8":
+                Wq, s, x, b, y = P
+                L.batch_fp8(Wq, s, x, b, y, M, N, K, v, stream)
+            elif self.fmt == "int4":
+                Wq, s, x, y = P
+                L.batch_int4(Wq, s, x, y, M, N, K, v, stream)
+            else:
+                Wq, s, z, x, b, y = P
+                L.batch_int4_zp(Wq, s, z, x, b, y, M, N, K, v, stream)
+            return self.copies[i]["y"]
         if self.fmt == "bf16":
             W, x, b, y = P
             if b is None:
@@ -121,6 +155,12 @@ class GemvCase:
         o = self.ops0
         idx = torch.arange(self.N) if rows is None else torch.as_tensor(rows, dtype=torch.long)
         x = o["x"].float()
+        if x.dim() == 2:                      # batch: one reference row per activation row
+            return torch.stack([self._reference_row(x[m], idx) for m in range(x.shape[0])])
+        return self._reference_row(x, idx)
+
+    def _reference_row(self, x, idx) -> torch.Tensor:
+        o = self.ops0
         out = torch.empty(len(idx), dtype=torch.float32)
         for a in range(0, len(idx), REF_ROWS):
             r = idx[a:a + REF_ROWS]
@@ -144,7 +184,7 @@ class GemvCase:
         torch.cuda.synchronize()
         y = y.cpu().float()
         if rows is not None:
-            y = y[torch.as_tensor(rows, dtype=torch.long)]
+            y = y[..., torch.as_tensor(rows, dtype=torch.long)]
         ref = self.reference(rows)
         refb = ref.to(torch.bfloat16).float()
         excess = ((y - refb).abs() - (atol + rtol * refb.abs())).max().item()

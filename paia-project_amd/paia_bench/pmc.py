@@ -53,7 +53,10 @@ def cmd_run(a) -> int:
     del src, dst
     lib = load_lib()
     N, K = map(int, a.shape.split("x"))
-    case = GemvCase(lib, a.fmt, N, K, bias=a.bias, variant=a.variant)
+    if a.batch:
+        case = GemvCase(lib, a.fmt, N, K, bias=a.bias, variant=a.variant, mode="batch", M=a.batch)
+    else:
+        case = GemvCase(lib, a.fmt, N, K, bias=a.bias, variant=a.variant)
     n = plan_rotation(case.footprint())["n_copies"]
     case.build(n, dev)
     chk = case.check(rows=list(range(min(N, 64))))
@@ -124,6 +127,7 @@ def main(argv=None) -> int:
     r.add_argument("--variant", type=int, default=None)
     r.add_argument("--bias", action="store_true")
     r.add_argument("--reps", type=int, default=20)
+    r.add_argument("--batch", type=int, default=0, help="M > 0: the small-batch kernels with M activation rows")
     s = sub.add_parser("summarize")
     s.add_argument("--fetch", required=True)
     s.add_argument("--write", required=True)

@@ -6,6 +6,7 @@ graph timing and rotation, keep the best and the top five), same tuned-table sch
 
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --out gpurun_out/sweep_fp8.json
     python -m paia_bench.sweep --fmt int4zp --shapes baseline --write-tuned paia-project_amd/tuned/mi355x.json
+    python -m paia_bench.sweep --fmt fp8 --shapes baseline --batch 1,2,4,8,16     # small-batch kernels (P,U,W,S)
 
 Copy 0 of each shape is checked against the CPU fp32 reference (sampled rows) for every variant before it is timed.
 """
@@ -50,7 +51,7 @@ def parse_filter(expr: str):
     import re
     conds = []
     for part in filter(None, (expr or "").split(",")):
-        m = re.fullmatch(r"([RUWSH])(>=|<=|=)(\d+)", part.strip())
+        m = re.fullmatch(r"([RUWSHPX])(>=|<=|=)(\d+)", part.strip())
         if not m:
             raise SystemExit(f"bad filter term {part!r}")
         conds.append((m.group(1), m.group(2), int(m.group(3))))
@@ -71,53 +72,78 @@ def main(argv=None):
     ap.add_argument("--samples", type=int, default=9)
     ap.add_argument("--out", default=None)
     ap.add_argument("--write-tuned", default=None)
+    ap.add_argument("--batch", default="", help="M values: time the small-batch kernels (variants P,U,W,S,X)")
+    ap.add_argument("--pick-only", action="store_true", help="time only the library's choice for each cell")
     a = ap.parse_args(argv)
 
     lib = load_lib()
     dev = torch.device("cuda:0")
-    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(a.fmt, lib.variants_int4)
+    batch = [int(m) for m in a.batch.split(",") if m]
+    if batch:
+        fam = lib.variants_batch[a.fmt]
+        knobs = "PUWSX"
+    else:
+        fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(a.fmt, lib.variants_int4)
+        knobs = "RUWSH"
     keep = parse_filter(a.variants)
     if a.shapes in ("baseline", "real", "all"):
         shapes = shape_set(a.shapes, a.fmt)
     else:
         shapes = [(s, *map(int, s.split("x"))) for s in a.shapes.split(",")]
+    cells = [(nm, N, K, M) for nm, N, K in shapes for M in (batch or [1])]
     results = {}
-    for nm, N, K in shapes:
-        case = GemvCase(lib, a.fmt, N, K, bias=(a.fmt != "int4" and nm.endswith("qkv") and K == 3584))
+    for nm, N, K, M in cells:
+        bias = a.fmt != "int4" and nm.endswith("qkv") and K == 3584
+        if batch:
+            case = GemvCase(lib, a.fmt, N, K, bias=bias, mode="batch", M=M)
+        else:
+            case = GemvCase(lib, a.fmt, N, K, bias=bias)
         rot = plan_rotation(case.footprint())
         t0 = time.time()
         case.build(rot["n_copies"], dev)
         rng = np.random.default_rng(0)
         rows = np.unique(np.concatenate([np.arange(min(N, 16)), N - 1 - np.arange(min(N, 16)),
                                          rng.integers(0, N, 64)])).astype(np.int32)
-        print(f"[sweep] {a.fmt} {nm} {N}x{K}: {rot['n_copies']} copies, built in {time.time() - t0:.1f}s", flush=True)
+        tag = f"M={M} " if batch else ""
+        print(f"[sweep] {a.fmt} {tag}{nm} {N}x{K}: {rot['n_copies']} copies, built in {time.time() - t0:.1f}s",
+              flush=True)
         rows_res = []
         for v in fam:
             if not keep(v):
                 continue
+            if a.pick_only and v["id"] != case.variant:
+                continue
             case.variant = v["id"]
-            chk = case.check(rows=rows)
+            try:
+                chk = case.check(rows=rows)
+            except RuntimeError as e:            # batch: S*M*U too large for the LDS chunk (-2)
+                print(f"  variant {v} refused: {e}", flush=True)
+                continue
             if not chk["ok"]:
                 print(f"  variant {v} INCORRECT {chk}", flush=True)
                 continue
             t = time_per_call_us(case.call, rot["n_copies"], target_ms=a.target_ms, samples=a.samples,
                                  warmup_ms=20.0)
             gbps = case.bytes()["total"] / (t["us"] * 1e-6) / 1e9
-            rows_res.append({"variant": {k: v[k] for k in "RUWSH"}, "id": v["id"], "us": t["us"], "gbps": gbps,
+            rows_res.append({"variant": {k: v[k] for k in knobs}, "id": v["id"], "us": t["us"], "gbps": gbps,
                              "cv": t.get("us_cv")})
-            print(f"  R={v['R']} U={v['U']} W={v['W']} S={v['S']} H={v['H']}: {t['us']:8.2f} us {gbps:7.0f} GB/s "
+            print("  " + " ".join(f"{k}={v[k]}" for k in knobs) + f": {t['us']:8.2f} us {gbps:7.0f} GB/s "
                   f"({100 * gbps / HBM_PEAK_GBPS:4.1f}%)", flush=True)
         rows_res.sort(key=lambda r: r["us"])
-        results[f"{N}x{K}"] = {"name": nm, "bytes": case.bytes()["total"], "ranked": rows_res}
+        key = f"{M}x{N}x{K}" if batch else f"{N}x{K}"
+        results[key] = {"name": nm, "M": M, "bytes": case.bytes()["total"], "ranked": rows_res,
+                        "pick": lib.batch_pick_variant(a.fmt, M, N, K) if batch else lib.pick_variant(a.fmt, N, K)}
         if rows_res:
             b = rows_res[0]
-            print(f"[best] {a.fmt} {nm} {N}x{K}: {b['variant']} {b['us']:.2f} us {b['gbps']:.0f} GB/s "
+            print(f"[best] {a.fmt} {tag}{nm} {N}x{K}: {b['variant']} {b['us']:.2f} us {b['gbps']:.0f} GB/s "
                   f"({100 * b['gbps'] / HBM_PEAK_GBPS:.1f}% of 8 TB/s)", flush=True)
         case.free()
         torch.cuda.empty_cache()
     if a.out:
         Path(a.out).parent.mkdir(parents=True, exist_ok=True)
         Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
+    if a.write_tuned and batch:
+        raise SystemExit("--write-tuned is for the M = 1 tables")
     if a.write_tuned:
         f = Path(a.write_tuned)
         tuned = json.loads(f.read_text()) if f.exists() else {"platform": "mi355x", "shapes": {}}

@@ -67,7 +67,7 @@ class GemvLib:
             "paia_gemv_bf16_variant_count": [],
             "paia_gemv_bf16_variant_info": [_I] + [ctypes.POINTER(_I)] * 5,
             "paia_gemv_batch_variant_count": [_I],
-            "paia_gemv_batch_variant_info": [_I, _I] + [ctypes.POINTER(_I)] * 4,
+            "paia_gemv_batch_variant_info": [_I, _I] + [ctypes.POINTER(_I)] * 5,
             "paia_gemv_batch_pick_variant": [_I, _I, _I, _I],
             "paia_gemv_batch_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
             "paia_gemv_batch_fp8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
@@ -94,9 +94,9 @@ class GemvLib:
         for kind, k in KINDS.items():
             vs = []
             for v in range(lib.paia_gemv_batch_variant_count(k)):
-                P, U, W, S = (_I() for _ in range(4))
-                assert lib.paia_gemv_batch_variant_info(k, v, *map(ctypes.byref, (P, U, W, S))) == 0
-                vs.append({"id": v, "P": P.value, "U": U.value, "W": W.value, "S": S.value})
+                P, U, W, S, X = (_I() for _ in range(5))
+                assert lib.paia_gemv_batch_variant_info(k, v, *map(ctypes.byref, (P, U, W, S, X))) == 0
+                vs.append({"id": v, "P": P.value, "U": U.value, "W": W.value, "S": S.value, "X": X.value})
             self.variants_batch[kind] = vs
 
     @staticmethod

@@ -27,9 +27,10 @@ LAYER = {
 LM_HEAD = {"llama31_8b": (128256, 4096), "qwen25_7b": (152064, 3584)}
 
 
-def gemv_bytes(fmt: str, N: int, K: int, bias: bool = False) -> dict:
-    """Algorithmic bytes of one GEMV: {weights, metadata, act_in, out, total}.
-    fmt: 'bf16' | 'fp8' | 'int4' (reference format: fp16 scales, zero 8) | 'int4zp' (bf16 scales + 4-bit zeros)."""
+def gemv_bytes(fmt: str, N: int, K: int, bias: bool = False, M: int = 1) -> dict:
+    """Algorithmic bytes of one GEMV with M activation rows: {weights, metadata, act_in, out, total}.
+    fmt: 'bf16' | 'fp8' | 'int4' (reference format: fp16 scales, zero 8) | 'int4zp' (bf16 scales + 4-bit zeros).
+    act_in = 2MK and out = 2MN, the reference harness's M accounting (paia-bench/bench/ops/cublas_bf16.py:18-21)."""
     G = K // 128
     if fmt == "bf16":
         w, meta = 2 * N * K, 0
@@ -41,6 +42,6 @@ def gemv_bytes(fmt: str, N: int, K: int, bias: bool = False) -> dict:
         w, meta = N * K // 2, 2 * N * G + N * ((G + 1) // 2)
     else:
         raise ValueError(fmt)
-    d = {"weights": w, "metadata": meta + (2 * N if bias else 0), "act_in": 2 * K, "out": 2 * N}
+    d = {"weights": w, "metadata": meta + (2 * N if bias else 0), "act_in": 2 * M * K, "out": 2 * M * N}
     d["total"] = sum(d.values())
     return d

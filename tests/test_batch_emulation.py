@@ -136,40 +136,37 @@ def test_int4_decode_constant_is_bf16_128():
 # ---------------------------------------------------------------------------------------------------------------
 # work decomposition
 # ---------------------------------------------------------------------------------------------------------------
-def plan(fmt, M, N, K, P, U, W, S):
-    """gemv_batch.h batch_plan + launch_batch (None when no chunk of U k-blocks fits)."""
-    i4 = fmt in ("int4", "int4zp")
+def plan(fmt, M, N, K, P, U, W, S, X=0):
+    """gemv_batch.h batch_plan + launch_batch (None when, X=0, no chunk of U k-blocks fits)."""
     KB = -(-K // 128)
     kbs = -(-KB // S)
-    per_kb = S * M * 256 + (S * 64 if i4 else 0)
+    cap = -(-kbs // U) * U
+    pb = (W // S) * (S - 1) * P * 1024 if S > 1 else 0
+    ntiles = -(-N // 16)
+    common = dict(KB=KB, kbs=kbs, ntiles=ntiles, grid=-(-ntiles // ((W // S) * P)))
+    if X == 1:
+        return dict(common, C=cap, nchunks=1, xrow=0, x_end=0, lds=pb)
+    per_kb = S * M * 256
     fixed = S * M * 16
     if fixed + per_kb * U > LDS:
         return None
-    C = (LDS - fixed) // per_kb
-    C -= C % U
-    C = min(C, -(-kbs // U) * U)
+    C = min((LDS - fixed) // per_kb // U * U, cap)
     xrow = C * 256 + 16
-    xb = fixed + per_kb * C
-    pb = (W // S) * (S - 1) * P * 1024 if S > 1 else 0
-    ntiles = -(-N // 16)
-    return dict(KB=KB, kbs=kbs, C=C, nchunks=-(-kbs // C), xrow=xrow, xs_off=S * M * xrow, lds=max(xb, pb),
-                ntiles=ntiles, grid=-(-ntiles // ((W // S) * P)))
+    return dict(common, C=C, nchunks=-(-kbs // C), xrow=xrow, x_end=S * M * xrow, lds=max(S * M * xrow, pb))
 
 
-def replay(fmt, M, N, K, P, U, W, S):
-    p = plan(fmt, M, N, K, P, U, W, S)
+def replay(fmt, M, N, K, P, U, W, S, X=0):
+    p = plan(fmt, M, N, K, P, U, W, S, X)
     assert p is not None
-    i4 = fmt in ("int4", "int4zp")
     seen = np.zeros((p["ntiles"], p["KB"]), dtype=np.int64)
     C, kbs = p["C"], p["kbs"]
     assert C % U == 0 and C >= U
-    # staging: vector q of chunk c -> (split, row, kbl, v); LDS addresses inside the x region
-    nvec = S * M * C * 16
-    assert (nvec - 1) // 16 // C // M < S
-    last = ((S - 1) * M + (M - 1)) * p["xrow"] + (C - 1) * 256 + 15 * 16 + 16
-    assert last <= p["xs_off"] <= p["lds"]
-    if i4:
-        assert p["xs_off"] + S * C * 16 * 4 <= p["lds"]
+    if X == 0:
+        # staging: vector q of chunk c -> (split, row, kbl, v); LDS addresses inside the x region
+        nvec = S * M * C * 16
+        assert (nvec - 1) // 16 // C // M < S
+        last = ((S - 1) * M + (M - 1)) * p["xrow"] + (C - 1) * 256 + 15 * 16 + 16
+        assert last <= p["x_end"] <= p["lds"]
     for b in range(p["grid"]):
         slots = set()
         for w in range(W):
@@ -188,7 +185,8 @@ def replay(fmt, M, N, K, P, U, W, S):
                             # the chunk slot read holds k-block split*kbs + c*C + kbl of this split
                             assert split * kbs + c * C + kbl == kb and kb < p["KB"]
                             # A-fragment reads stay in the split's rows of this chunk
-                            assert (split * M + M - 1) * p["xrow"] + kbl * 256 + 256 <= p["xs_off"]
+                            if X == 0:
+                                assert (split * M + M - 1) * p["xrow"] + kbl * 256 + 256 <= p["x_end"]
                             for tt in range(P):
                                 if tile0 + tt < p["ntiles"]:
                                     seen[tile0 + tt, kb] += 1
@@ -217,26 +215,26 @@ def test_every_tile_and_k_block_once(fmt):
     shapes = [(1, 16 * 1 + 3, 128), (3, 100, 3 * 128), (2, 257, 1000 // kmult * kmult), (16, 64, 4096),
               (16, 40, 14336), (7, 4608, 3584), (5, 33, 18944)]
     n = 0
-    for (M, N, K), (P, U), (W, S) in itertools.product(shapes, TABLE[fmt], WS):
-        if K % kmult or plan(fmt, M, N, K, P, U, W, S) is None:
+    for (M, N, K), (P, U), (W, S), X in itertools.product(shapes, TABLE[fmt], WS, (0, 1)):
+        if K % kmult or plan(fmt, M, N, K, P, U, W, S, X) is None:
             continue
-        replay(fmt, M, N, K, P, U, W, S)
+        replay(fmt, M, N, K, P, U, W, S, X)
         n += 1
-    assert n > 50
+    assert n > 100
 
 
 def test_table_matches_library(gemv_lib):
     """The variant tables replayed here are the library's, and the library's default pick always has a plan."""
     L = gemv_lib
     for fmt, k in KINDS.items():
-        got = {(v["P"], v["U"], v["W"], v["S"]) for v in L.variants_batch[fmt]}
-        want = {(P, U, W, S) for (P, U), (W, S) in itertools.product(TABLE[fmt], WS)}
+        got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
+        want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
         assert got == want, fmt
         for M in (1, 2, 4, 8, 16):
             for N, K in [(4096, 4096), (28672, 4096), (4096, 14336), (4608, 3584), (3584, 18944), (128256, 4096)]:
                 v = L.batch_pick_variant(fmt, M, N, K)
                 assert 0 <= v < len(L.variants_batch[fmt])
                 d = L.variants_batch[fmt][v]
-                assert plan(fmt, M, N, K, d["P"], d["U"], d["W"], d["S"]) is not None
+                assert plan(fmt, M, N, K, d["P"], d["U"], d["W"], d["S"], d["X"]) is not None
         assert L.batch_pick_variant(fmt, 17, 4096, 4096) == -1
         assert L.batch_pick_variant(fmt, 0, 4096, 4096) == -1

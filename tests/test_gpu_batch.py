@@ -106,7 +106,7 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
             refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
             xd = x.to(cuda)
             for v in gemv_lib.variants_batch[fmt]:
-                if plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"]) is None:
+                if plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"]) is None:
                     # S*M*U too large for the LDS chunk: the entry point refuses it (-2) before launching
                     with pytest.raises(RuntimeError, match="code -2"):
                         run_batch(gemv_lib, fmt, dev, xd, v["id"])
@@ -144,7 +144,9 @@ def test_rows_independent_and_deterministic(gemv_lib, cuda, fmt):
     dev = to_device(ops, cuda)
     x = x_rows(16, K, 77).to(cuda)
     vs = gemv_lib.variants_batch[fmt]
-    picks = [next(v["id"] for v in vs if v["S"] == 1), next(v["id"] for v in vs if v["S"] == 4 and v["U"] == 2)]
+    picks = [next(v["id"] for v in vs if v["S"] == 1 and v["X"] == 0),
+             next(v["id"] for v in vs if v["S"] == 4 and v["U"] == 2 and v["X"] == 0),
+             next(v["id"] for v in vs if v["S"] == 8 and v["X"] == 1)]
     for vid in picks:
         note(f"batch rows-independent {fmt} variant={vs[vid]}")
         y16 = run_batch(gemv_lib, fmt, dev, x, vid)
@@ -213,7 +215,7 @@ def test_graph_capture_replays_match_eager(gemv_lib, cuda):
     o, _ = make("fp8", N, K)
     d = to_device(o, cuda)
     x = x_rows(4, K, 9).to(cuda)
-    vid = next(v["id"] for v in gemv_lib.variants_batch["fp8"] if v["S"] == 4 and v["U"] == 2)
+    vid = next(v["id"] for v in gemv_lib.variants_batch["fp8"] if v["S"] == 4 and v["U"] == 2 and v["X"] == 0)
     eager = run_batch(gemv_lib, "fp8", d, x, vid)
     torch.cuda.synchronize()
     y = torch.empty_like(eager)
