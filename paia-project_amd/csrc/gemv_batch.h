@@ -374,7 +374,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
                 float o = acc[t][v];
                 if constexpr (F == kFP8) o = o * __uint_as_float(ep_scale[t]);
                 if (p.bias) o = o + bf16_to_f32(ep_bias[t]);
-                p.y[(size_t)m * (size_t)p.N + (size_t)row] = (uint16_t)f32_to_bf16_rne(o);
+                p.y[(size_t)m * (size_t)p.N + (size_t)row] = (uint16_t)f32_to_bf16_out(o);
             }
         }
     }

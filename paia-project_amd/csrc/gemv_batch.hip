@@ -72,7 +72,8 @@ bool fits(const BatchVariant& v, int M)
 //   * split-K S: the fewest splits (<= 8, >= 2 k-blocks each) that give >= 3072 waves (12 per CU);
 //   * x in LDS (X=0) unless the splits x rows make staging cost more than it saves (M*S >= 32 with S >= 4: each block
 //     would stage half or more of its weight bytes again as x) or not even one chunk of U k-blocks fits;
-//   * one tile per wave; two when x comes with the weights and M >= 4, so the two tiles share each x load.
+//   * one tile per wave; two when x comes with the weights and M >= 8, so the two tiles share each x load (at M = 4
+//     the halved wave count costs more than the shared loads save).
 int pick(int kind, int M, int N, int K)
 {
     const Table t = table(kind);
@@ -85,7 +86,7 @@ int pick(int kind, int M, int N, int K)
     int P = 1, U = kind >= 2 ? 4 : 2;
     int X = 0;
     if ((M * S >= 32 && S >= 4) || batch_x_bytes(S, M, U) > kBatchLds) X = 1;
-    if (X == 1 && M >= 4) {
+    if (X == 1 && M >= 8) {
         P = 2;
         U = kind >= 2 ? 4 : 2;
     }

@@ -71,12 +71,20 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16)
     return (float)__builtin_bit_cast(_Float16, (unsigned short)h16);
 }
 
-// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN. Integer form, used where the exact bits are part
+// of a stored format (quantizer scales).
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f)
 {
     const uint32_t u = __float_as_uint(f);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// The same rounding in one instruction (gfx950 v_cvt_pk_bf16_f32, round to nearest even in the default mode; NaN
+// becomes a quiet NaN), for output epilogues: no branch, so a store lane needs no exec-mask juggling.
+__device__ __forceinline__ uint32_t f32_to_bf16_out(float f)
+{
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
 }
 
 // Two e4m3fn bytes (byte pair HI of word w) -> two bf16, exact for every code. v_cvt_pk_f32_fp8 (OCP e4m3 on
@@ -163,6 +171,22 @@ __device__ __forceinline__ float wave_sum(float v)
     v = dpp_add<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3 -> lane 63 holds the total
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// Two wave sums at once: v_permlane32_swap pairs the upper half of a with the lower half of b, so one add leaves
+// half-sums of a in lanes 0-31 and of b in lanes 32-63; four DPP adds make 16-lane row sums and row_bcast:15 adds
+// row 0 into row 1 and row 2 into row 3. Lane 31 ends with sum(a), lane 63 with sum(b): 7 VALU for two rows where
+// wave_sum takes 12 and two readlanes. Fixed order, so bitwise reproducible.
+__device__ __forceinline__ float wave_sum2(float a, float b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    float v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    v = dpp_add<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add<0x124, 0xF>(v);   // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);   // row_ror:8
+    v = dpp_add<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+    return v;
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v)
 {

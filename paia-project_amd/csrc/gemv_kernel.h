@@ -319,10 +319,14 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     auto finish = [&](const Item<F, R, U>& B) {
         float tot[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            tot[r] = wave_sum(acc[r]);
-            acc[r] = 0.0f;
+        for (int r = 0; r + 1 < R; r += 2) {
+            const float v = wave_sum2(acc[r], acc[r + 1]);
+            tot[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+            tot[r + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
         }
+        if constexpr (R & 1) tot[R - 1] = wave_sum(acc[R - 1]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
         if constexpr (!KSPLIT) {
             // lanes kk*R .. kk*R+R-1 hold this group's epilogue operands (kk = the group's slot in the window) and
             // store its R rows: one store instruction per group
@@ -336,7 +340,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
             if (r >= 0 && r < R && row < p.N) {
                 if constexpr (F == kFP8) v = v * __uint_as_float(ep_scale);
                 if (p.bias) v = v + bf16_to_f32(ep_bias);
-                p.y[row] = (uint16_t)f32_to_bf16_rne(v);
+                p.y[row] = (uint16_t)f32_to_bf16_out(v);
             }
         } else {
             if (lane < R) {
@@ -363,7 +367,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
             if (row < p.N) {
                 if constexpr (F == kFP8) v = v * reinterpret_cast<const float*>(p.meta)[row];
                 if (p.bias) v = v + bf16_to_f32(p.bias[row]);
-                p.y[row] = (uint16_t)f32_to_bf16_rne(v);
+                p.y[row] = (uint16_t)f32_to_bf16_out(v);
             }
         }
         __syncthreads();

@@ -79,7 +79,7 @@ def _per_kernel(path: Path, counter: str) -> dict:
                 continue
             name = r["Kernel_Name"]
             short = ("read_probe" if "read_probe_kernel" in name else "copy_probe" if "copy_probe_kernel" in name
-                     else name.split("(")[0].replace("void ", "") if "paia::" in name else None)
+                     else name.split("(")[0].replace("void ", "") if "paia::gemv" in name else None)
             if short is None:
                 continue
             out.setdefault(short, []).append(float(r["Counter_Value"]))

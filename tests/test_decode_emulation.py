@@ -103,3 +103,62 @@ def test_fp8_upper_half_packing_exact_for_every_code():
     finite = ~np.isnan(f)
     assert np.array_equal(dec[finite], f[finite])
     assert np.isnan(dec[~finite]).all() and (~finite).sum() == 2        # 0x7F and 0xFF stay NaN
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# wave reductions (gemv_device.h wave_sum / wave_sum2): lane-exact emulation of the DPP and permlane network
+# ---------------------------------------------------------------------------------------------------------------
+def dpp_add(v, ctrl, row_mask):
+    """v + update_dpp(old=0, v, ctrl, row_mask): lanes of rows outside row_mask add 0."""
+    v = np.asarray(v, dtype=np.float64)
+    src = np.zeros(64)
+    for i in range(64):
+        row, j = divmod(i, 16)
+        if ctrl == 0xB1:
+            s = (i & ~3) | ((i & 3) ^ 1)
+        elif ctrl == 0x4E:
+            s = (i & ~3) | ((i & 3) ^ 2)
+        elif ctrl in (0x124, 0x128):
+            n = ctrl & 0xF
+            s = row * 16 + (j - n) % 16
+        elif ctrl == 0x142:          # row_bcast:15 -> lane 15 of the previous row
+            s = (row - 1) * 16 + 15 if row > 0 else None
+        elif ctrl == 0x143:          # row_bcast:31 -> lane 31
+            s = 31 if row > 1 else None
+        else:
+            raise ValueError(ctrl)
+        src[i] = v[s] if ((row_mask >> row) & 1) and s is not None else 0.0
+    return v + src
+
+
+def wave_sum_lanes(v):
+    for ctrl, mask in [(0xB1, 0xF), (0x4E, 0xF), (0x124, 0xF), (0x128, 0xF), (0x142, 0xA), (0x143, 0xC)]:
+        v = dpp_add(v, ctrl, mask)
+    return v
+
+
+def wave_sum2_lanes(a, b):
+    """v_permlane32_swap(a, b): a keeps lanes 0-31 and takes b's lanes 0-31 in 32-63; b takes a's 32-63 in 0-31."""
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    a2 = np.concatenate([a[:32], b[:32]])
+    b2 = np.concatenate([a[32:], b[32:]])
+    v = a2 + b2
+    for ctrl, mask in [(0xB1, 0xF), (0x4E, 0xF), (0x124, 0xF), (0x128, 0xF), (0x142, 0xA)]:
+        v = dpp_add(v, ctrl, mask)
+    return v
+
+
+def test_wave_reductions_sum_every_lane_once():
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        a = rng.integers(-1000, 1000, 64).astype(np.float64)
+        b = rng.integers(-1000, 1000, 64).astype(np.float64)
+        assert wave_sum_lanes(a)[63] == a.sum()
+        v = wave_sum2_lanes(a, b)
+        assert v[31] == a.sum() and v[63] == b.sum()
+    # each lane's contribution counted exactly once (unit vectors)
+    for i in range(64):
+        e = np.zeros(64)
+        e[i] = 1.0
+        assert wave_sum_lanes(e)[63] == 1.0
+        assert wave_sum2_lanes(e, 2 * e)[31] == 1.0 and wave_sum2_lanes(e, 2 * e)[63] == 2.0
