@@ -229,8 +229,10 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         bound_g = g;
     };
 
-    // H=0 epilogue operands, loaded once per wave (per window of ep_groups groups): lane kk*R + r holds FP8 scale and
-    // bias of row r of the wave's group number (window*ep_groups + kk). Rows past N or past the wave's groups read 0.
+    // H=0 epilogue operands, loaded once per wave before the streaming loop: lane kk*R + r holds FP8 scale and bias
+    // of row r of the wave's group number kk. The launch gives no wave more than ep_groups = 64/R groups, so one
+    // load covers them all and the loop holds no conditional load (a load under a branch there makes the compiler
+    // wait for every outstanding load, draining the prefetched items at every row). Rows past N read 0.
     constexpr int ep_groups = kWave / R;
     uint32_t ep_scale = 0u, ep_bias = 0u;
     auto ep_load = [&](int k_first) {
@@ -330,8 +332,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         if constexpr (!KSPLIT) {
             // lanes kk*R .. kk*R+R-1 hold this group's epilogue operands (kk = the group's slot in the window) and
             // store its R rows: one store instruction per group
-            const int kk = B.k % ep_groups;
-            if (kk == 0 && B.k > 0) ep_load(B.k);   // next window (only for waves with more than 64/R groups)
+            const int kk = B.k;   // < ep_groups (launch_gemv caps the groups per wave)
             const int r = lane - kk * R;
             float v = tot[0];
 #pragma unroll
@@ -387,15 +388,14 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     x_store<F, XE>(p, xr, xs, s32);
     __syncthreads();
 
+    // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
+    // loop header without the other buffer's loads would make the compiler's wait counts assume those loads absent,
+    // and every consume would then wait for all outstanding loads (vmcnt(0)), the prefetched item included.
     if constexpr (!KSPLIT) {
-        bool done = buf[0].group < 0;
-        while (!done) {
+        for (;;) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                if (buf[d].group < 0) {
-                    done = true;
-                    break;
-                }
+                if (buf[d].group < 0) return;
                 consume(buf[d]);
                 if (buf[d].last) finish(buf[d]);
                 issue(buf[d]);
@@ -407,14 +407,10 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
         const int ngb = (int)blockIdx.x < p.ngroups ? (p.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
         int k_done = 0;
         if (buf[0].group >= 0) {
-            bool done = false;
-            while (!done) {
+            for (;;) {
 #pragma unroll
                 for (int d = 0; d < D; ++d) {
-                    if (buf[d].group < 0) {
-                        done = true;
-                        break;
-                    }
+                    if (buf[d].group < 0) return;   // every round this wave takes part in is combined by now
                     consume(buf[d]);
                     if (buf[d].last) {
                         finish(buf[d]);
@@ -512,7 +508,10 @@ int launch_gemv(GemvParams p, hipStream_t st)
     const int per_block_units = KSPLIT ? 1 : W;
     int grid = (p.ngroups + per_block_units - 1) / per_block_units;
     if (grid > gmax) grid = gmax;
-    const int q = (p.ngroups + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
+    int q = (p.ngroups + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
+    // H=0: at most 64/R row groups per wave, so the wave's epilogue operands fit one register (beyond that the
+    // grid grows past one resident wave of blocks)
+    if (!KSPLIT && q > kWave / R) q = kWave / R;
     grid = (p.ngroups + q * per_block_units - 1) / (q * per_block_units);
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();

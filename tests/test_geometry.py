@@ -58,6 +58,8 @@ def launch(fmt, N, K, R, U, W, H, cus, per_cu):
     unit = 1 if H else W
     grid = min(-(-p["ngroups"] // unit), gmax)
     q = -(-p["ngroups"] // (grid * unit))
+    if not H:
+        q = min(q, 64 // R)          # epilogue operands of all of a wave's groups in one register
     grid = -(-p["ngroups"] // (q * unit))
     p["grid"] = grid
     p["round"] = rnd
@@ -103,6 +105,8 @@ def replay(fmt, N, K, R, U, W, H, cus=256, per_cu=4):
                 if last:
                     finished += 1
                     if not H:
+                        # the store lanes k*R + r hold the group's epilogue operands: k must fit one register
+                        assert k < 64 // R, f"wave group index {k} beyond the epilogue register (R={R})"
                         for r in range(R):
                             if g * R + r < N:
                                 stored[g * R + r] += 1
@@ -171,3 +175,10 @@ def test_lds_limit_matches_contract():
     assert launch("fp8", 8, 32768, 1, 1, 4, 0, 256, 1) is not None
     assert launch("int4", 8, 30720, 1, 1, 4, 0, 256, 1) is not None
     assert launch("int4", 8, 30848, 1, 1, 4, 0, 256, 1) is None
+
+
+def test_groups_per_wave_capped_for_the_epilogue_register():
+    """Tall N on a small grid: without the cap a wave would own more than 64/R groups (its epilogue operands would
+    not fit the one register loaded before the streaming loop); the launch grows the grid instead."""
+    for R, U, W in [(1, 1, 4), (2, 2, 4), (4, 1, 8), (8, 1, 4)]:
+        replay("fp8", 40000, 256, R, U, W, 0, cus=2, per_cu=1)
