@@ -145,10 +145,13 @@ struct Item {
 // Item buffers in flight per wave. Two: measured on MI355X, deeper pipelines of small items (8 x 1 KiB, 4 x 2 KiB)
 // were slower than two buffers of larger items (2 x 4 KiB) at the same bytes in flight, because every item pays
 // its issue/offset/epilogue bookkeeping; the bytes in flight are set by the item size R*U instead.
+#ifndef PAIA_GEMV_PIPE_DEPTH
+#define PAIA_GEMV_PIPE_DEPTH 2
+#endif
 template <int R, int U>
 __host__ __device__ constexpr int pipe_depth()
 {
-    return 2;
+    return PAIA_GEMV_PIPE_DEPTH;
 }
 
 // Walks a wave's items in order. H=0: groups g = first + k*gstride (k = 0..), every segment of each in turn.

@@ -140,19 +140,22 @@ def plan(fmt, M, N, K, P, U, W, S, X=0):
     """gemv_batch.h batch_plan + launch_batch (None when, X=0, no chunk of U k-blocks fits)."""
     KB = -(-K // 128)
     kbs = -(-KB // S)
+    mg = 4 if fmt in ("int4", "int4zp") and U % 4 == 0 and KB % 4 == 0 else 1
+    if mg == 4:
+        kbs = -(-kbs // 4) * 4           # grouped metadata: every split starts on a four-group boundary
     cap = -(-kbs // U) * U
     pb = (W // S) * (S - 1) * P * 1024 if S > 1 else 0
     ntiles = -(-N // 16)
     common = dict(KB=KB, kbs=kbs, ntiles=ntiles, grid=-(-ntiles // ((W // S) * P)))
     if X == 1:
-        return dict(common, C=cap, nchunks=1, xrow=0, x_end=0, lds=pb)
+        return dict(common, C=cap, nchunks=1, xrow=0, x_end=0, lds=pb, mg=mg)
     per_kb = S * M * 256
     fixed = S * M * 16
     if fixed + per_kb * U > LDS:
         return None
     C = min((LDS - fixed) // per_kb // U * U, cap)
     xrow = C * 256 + 16
-    return dict(common, C=C, nchunks=-(-kbs // C), xrow=xrow, x_end=S * M * xrow, lds=max(S * M * xrow, pb))
+    return dict(common, C=C, nchunks=-(-kbs // C), xrow=xrow, x_end=S * M * xrow, lds=max(S * M * xrow, pb), mg=mg)
 
 
 def replay(fmt, M, N, K, P, U, W, S, X=0):
@@ -180,6 +183,8 @@ def replay(fmt, M, N, K, P, U, W, S, X=0):
                         break
                     for u in range(U):
                         kbl, t = kbl0 + u, c * C + kbl0 + u
+                        if p["mg"] == 4:
+                            assert (kb0 + t) % 4 == u % 4, "grouped metadata stage slot out of step with its groups"
                         if kbl < t_end:
                             kb = kb0 + t
                             # the chunk slot read holds k-block split*kbs + c*C + kbl of this split
@@ -203,7 +208,7 @@ def replay(fmt, M, N, K, P, U, W, S, X=0):
 TABLE = {
     "bf16": [(1, 2), (1, 4), (2, 2)],
     "fp8": [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4), (4, 2)],
-    "int4": [(1, 4), (1, 8), (2, 2), (2, 4), (2, 8), (4, 2), (4, 4)],
+    "int4": [(1, 4), (1, 8), (2, 2), (2, 4), (4, 2), (4, 4)],
 }
 TABLE["int4zp"] = TABLE["int4"]
 WS = [(4, 1), (4, 2), (4, 4), (8, 1), (8, 2), (8, 4), (8, 8)]
