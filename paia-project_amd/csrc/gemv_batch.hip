@@ -70,11 +70,23 @@ bool fits(const BatchVariant& v, int M)
 }
 
 // Default choice, fitted to MI355X sweeps of the Llama/Qwen projection shapes at M = 1, 4, 16 (FP8 and INT4):
-//   * split-K S: the fewest splits (<= 8, >= 2 k-blocks each) that give >= 3072 waves (12 per CU);
+//   * split-K S: at least two splits (every shape streamed faster with two waves per tile than with one), then the
+//     fewest (<= 8, >= 2 k-blocks each) that give >= 1152 work units (tiles x splits, 4.5 per CU): qkv (384 tiles)
+//     measured best at S = 4, o/down (256 tiles) at S = 8, gate_up (1792 tiles) at S = 2;
 //   * x in LDS (X=0) unless the splits x rows make staging cost more than it saves (M*S >= 32 with S >= 4: each block
 //     would stage half or more of its weight bytes again as x) or not even one chunk of U k-blocks fits;
-//   * one tile per wave; two when x comes with the weights and M >= 8, so the two tiles share each x load (at M = 4
-//     the halved wave count costs more than the shared loads save).
+//   * one tile per wave; two when x comes with the weights and M >= 8, so the two tiles share each x load, provided
+//     the halved tile count still gives >= 1152 units within 8 splits (at 256 tiles it does not, and one tile per
+//     wave was faster there).
+constexpr int kPickUnits = 1152;
+
+int pick_splits(int units0, int KB, int W)
+{
+    int S = 1;
+    while (S < W && (S == 1 || units0 * S < kPickUnits) && (KB + 2 * S - 1) / (2 * S) >= 2) S *= 2;
+    return S;
+}
+
 int pick(int kind, int M, int N, int K)
 {
     const Table t = table(kind);
@@ -82,14 +94,17 @@ int pick(int kind, int M, int N, int K)
     const int W = 8;
     const int ntiles = (N + kTileRows - 1) / kTileRows;
     const int KB = (K + kBlockCols - 1) / kBlockCols;
-    int S = 1;
-    while (S < W && ntiles * S < 3072 && (KB + 2 * S - 1) / (2 * S) >= 2) S *= 2;
-    int P = 1, U = kind >= 2 ? 4 : 2;
-    int X = 0;
+    const int U = kind >= 2 ? 4 : 2;
+    int S = pick_splits(ntiles, KB, W);
+    int P = 1, X = 0;
     if ((M * S >= 32 && S >= 4) || batch_x_bytes(S, M, U) > kBatchLds) X = 1;
     if (X == 1 && M >= 8) {
-        P = 2;
-        U = kind >= 2 ? 4 : 2;
+        const int pairs = (ntiles + 1) / 2;
+        const int S2 = pick_splits(pairs, KB, W);
+        if (pairs * S2 >= kPickUnits) {
+            P = 2;
+            S = S2;
+        }
     }
     return find(t, P, U, W, S, X);
 }

@@ -111,19 +111,14 @@ bool int4_args_ok(const void* Wq, const void* scales, const void* x, const void*
 // R=2 U=4 W=4 S=0 H=1, looked up by its knobs (as src/paia_gemv/gemv_quant.cu:47-56 does).
 int default_bf16_variant()
 {
-    static int v = -1;
-    if (v < 0) {
-        int found = 0;
+    static const int v = [] {   // thread-safe one-time initialisation
         for (int i = 0; i < paia_gemv_bf16_variant_count(); ++i) {
             int R, U, W, S, H;
             paia_gemv_bf16_variant_info(i, &R, &U, &W, &S, &H);
-            if (R == 2 && U == 4 && W == 4 && S == 0 && H == 1) {
-                found = i;
-                break;
-            }
+            if (R == 2 && U == 4 && W == 4 && S == 0 && H == 1) return i;
         }
-        v = found;
-    }
+        return 0;
+    }();
     return v;
 }
 

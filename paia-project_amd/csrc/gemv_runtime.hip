@@ -10,9 +10,10 @@ namespace paia {
 
 DeviceFacts device_facts()
 {
+    // cus is published last (release) and read first (acquire), so a reader that sees it also sees lds
     static std::atomic<int> cus{0}, lds{0};
     DeviceFacts f;
-    f.cus = cus.load(std::memory_order_relaxed);
+    f.cus = cus.load(std::memory_order_acquire);
     f.lds_per_cu = lds.load(std::memory_order_relaxed);
     if (f.cus == 0) {
         int dev = 0, n = 0, l = 0;
@@ -22,8 +23,8 @@ DeviceFacts device_facts()
         }
         f.cus = n > 0 ? n : 256;
         f.lds_per_cu = l > 0 ? l : 65536;
-        cus.store(f.cus, std::memory_order_relaxed);
         lds.store(f.lds_per_cu, std::memory_order_relaxed);
+        cus.store(f.cus, std::memory_order_release);
     }
     return f;
 }

@@ -38,6 +38,23 @@ void* stream_of(const at::Tensor& t)
 
 constexpr int64_t kMaxRows = 16;   // activation rows the small-batch kernels take
 
+// Every operand must live on the GPU the kernel runs on: the kernels dereference the raw pointers, so a host tensor
+// (the dispatcher picks the GPU kernel when any argument is on the GPU) or another GPU's tensor must be refused here.
+void on_device_of(const at::Tensor& W, const at::Tensor& t, const char* name)
+{
+    TORCH_CHECK(t.device() == W.device(), name, " must be on the device of the weights (", W.device(), "), found ",
+                t.device());
+}
+void on_device_of(const at::Tensor& W, const std::optional<at::Tensor>& t, const char* name)
+{
+    if (t.has_value()) on_device_of(W, *t, name);
+}
+void check_weights(const at::Tensor& W, int64_t N, int64_t K)
+{
+    TORCH_CHECK(W.is_cuda(), "the weights must be on a GPU, found ", W.device());
+    TORCH_CHECK(N <= INT32_MAX && K <= INT32_MAX, "N and K must fit in 32 bits (the C ABI takes int)");
+}
+
 int64_t x_len(const at::Tensor& x)
 {
     TORCH_CHECK(x.dim() == 1 || (x.dim() == 2 && x.size(0) >= 1 && x.size(0) <= kMaxRows),
@@ -59,7 +76,6 @@ void check_out(const at::Tensor& out, const at::Tensor& x, int64_t N)
 {
     TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.is_contiguous() && out.numel() == x_rows(x) * N,
                 "out must be a contiguous bfloat16 tensor with M*N elements");
-    TORCH_CHECK(out.device() == x.device(), "out must be on the device of x");
 }
 
 const void* opt_ptr(const std::optional<at::Tensor>& t, int64_t N)
@@ -81,8 +97,12 @@ void gemv_bf16_out(const at::Tensor& W, const at::Tensor& x, const std::optional
 {
     TORCH_CHECK(W.dim() == 2 && W.scalar_type() == at::kBFloat16 && W.is_contiguous(), "W must be bf16 [N, K]");
     const int64_t N = W.size(0), K = W.size(1);
+    check_weights(W, N, K);
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
+    on_device_of(W, x, "x");
+    on_device_of(W, bias, "bias");
+    on_device_of(W, out, "out");
     c10::DeviceGuard g(W.device());
     const int64_t M = x_rows(x);
     if (M > 1) {
@@ -107,9 +127,14 @@ void gemv_fp8_out(const at::Tensor& Wq, const at::Tensor& scale, const at::Tenso
 {
     TORCH_CHECK(Wq.dim() == 2 && Wq.element_size() == 1 && Wq.is_contiguous(), "Wq must be 1-byte e4m3 [N, K]");
     const int64_t N = Wq.size(0), K = Wq.size(1);
+    check_weights(Wq, N, K);
     TORCH_CHECK(scale.scalar_type() == at::kFloat && scale.numel() == N && scale.is_contiguous(), "scale: fp32 [N]");
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
+    on_device_of(Wq, scale, "scale");
+    on_device_of(Wq, x, "x");
+    on_device_of(Wq, bias, "bias");
+    on_device_of(Wq, out, "out");
     c10::DeviceGuard g(Wq.device());
     const int64_t M = x_rows(x);
     if (M > 1) {
@@ -143,10 +168,14 @@ void gemv_int4_out(const at::Tensor& Wq, const at::Tensor& scales, const at::Ten
                    at::Tensor& out)
 {
     const int64_t N = Wq.size(0), K = int4_K(Wq);
+    check_weights(Wq, N, K);
     TORCH_CHECK(scales.scalar_type() == at::kHalf && scales.is_contiguous() && scales.numel() == N * (K / 128),
                 "scales: fp16 [N, K/128]");
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
+    on_device_of(Wq, scales, "scales");
+    on_device_of(Wq, x, "x");
+    on_device_of(Wq, out, "out");
     c10::DeviceGuard g(Wq.device());
     const int64_t M = x_rows(x);
     if (M > 1) {
@@ -170,12 +199,18 @@ void gemv_int4_zp_out(const at::Tensor& Wq, const at::Tensor& scales, const at::
                       const std::optional<at::Tensor>& bias, int64_t variant, at::Tensor& out)
 {
     const int64_t N = Wq.size(0), K = int4_K(Wq), G = K / 128;
+    check_weights(Wq, N, K);
     TORCH_CHECK(scales.scalar_type() == at::kBFloat16 && scales.is_contiguous() && scales.numel() == N * G,
                 "scales: bf16 [N, K/128]");
     TORCH_CHECK(zeros.scalar_type() == at::kByte && zeros.is_contiguous() && zeros.numel() == N * ((G + 1) / 2),
                 "zeros: uint8 [N, ceil(K/256)] (two 4-bit zero points per byte along the groups)");
     TORCH_CHECK(x_len(x) == K, "x length must equal K");
     check_out(out, x, N);
+    on_device_of(Wq, scales, "scales");
+    on_device_of(Wq, zeros, "zeros");
+    on_device_of(Wq, x, "x");
+    on_device_of(Wq, bias, "bias");
+    on_device_of(Wq, out, "out");
     c10::DeviceGuard g(Wq.device());
     const int64_t M = x_rows(x);
     if (M > 1) {
@@ -201,7 +236,9 @@ at::Tensor dequant_fp8(const at::Tensor& Wq, const at::Tensor& scale)
 {
     TORCH_CHECK(Wq.dim() == 2 && Wq.element_size() == 1 && Wq.is_contiguous(), "Wq must be 1-byte e4m3 [N, K]");
     const int64_t N = Wq.size(0), K = Wq.size(1);
+    check_weights(Wq, N, K);
     TORCH_CHECK(scale.scalar_type() == at::kFloat && scale.numel() == N && scale.is_contiguous(), "scale: fp32 [N]");
+    on_device_of(Wq, scale, "scale");
     at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
     c10::DeviceGuard g(Wq.device());
     check_rc(paia_dequant_fp8(Wq.data_ptr(), scale.data_ptr(), out.data_ptr(), (int)N, (int)K, stream_of(Wq)),
@@ -214,6 +251,8 @@ at::Tensor dequant_int4(const at::Tensor& Wq, const at::Tensor& scales)
     const int64_t N = Wq.size(0), K = int4_K(Wq);
     TORCH_CHECK(scales.scalar_type() == at::kHalf && scales.is_contiguous() && scales.numel() == N * (K / 128),
                 "scales: fp16 [N, K/128]");
+    check_weights(Wq, N, K);
+    on_device_of(Wq, scales, "scales");
     at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
     c10::DeviceGuard g(Wq.device());
     check_rc(paia_dequant_int4(Wq.data_ptr(), scales.data_ptr(), out.data_ptr(), (int)N, (int)K, stream_of(Wq)),
@@ -228,6 +267,9 @@ at::Tensor dequant_int4_zp(const at::Tensor& Wq, const at::Tensor& scales, const
                 "scales: bf16 [N, K/128]");
     TORCH_CHECK(zeros.scalar_type() == at::kByte && zeros.is_contiguous() && zeros.numel() == N * ((G + 1) / 2),
                 "zeros: uint8 [N, ceil(K/256)]");
+    check_weights(Wq, N, K);
+    on_device_of(Wq, scales, "scales");
+    on_device_of(Wq, zeros, "zeros");
     at::Tensor out = at::empty({N, K}, Wq.options().dtype(at::kFloat));
     c10::DeviceGuard g(Wq.device());
     check_rc(paia_dequant_int4_zp(Wq.data_ptr(), scales.data_ptr(), zeros.data_ptr(), out.data_ptr(), (int)N, (int)K,
@@ -241,6 +283,7 @@ void check_w32(const at::Tensor& W, int64_t kmult)
 {
     TORCH_CHECK(W.dim() == 2 && W.scalar_type() == at::kFloat && W.is_contiguous(), "W must be contiguous fp32 [N, K]");
     TORCH_CHECK(W.size(1) % kmult == 0, "K must be a multiple of ", kmult);
+    check_weights(W, W.size(0), W.size(1));
 }
 
 std::tuple<at::Tensor, at::Tensor> quantize_fp8_rowwise(const at::Tensor& W)

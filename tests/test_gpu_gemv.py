@@ -246,3 +246,28 @@ def test_graph_capture_replays_match_eager(oracle, gemv_lib, cuda):
         for fmt, _, _, eager, y in cases:
             assert np.array_equal(bits16(y), eager), f"replay {rep} {fmt}"
         del junk
+
+
+def test_torch_ops_refuse_operands_off_the_weight_device(cuda):
+    """The torch ops run whenever any argument is on the GPU, so an operand left in host memory must be refused
+    before a kernel could dereference its pointer: x, scale, bias or out on the CPU -> RuntimeError, nothing launched."""
+    from paia_gemv import ops
+    ops.load()
+    N, K = 64, 1024
+    Wq = torch.zeros(N, K, dtype=torch.uint8, device=cuda)
+    scale = torch.ones(N, dtype=torch.float32, device=cuda)
+    x = torch.zeros(K, dtype=torch.bfloat16, device=cuda)
+    bias = torch.zeros(N, dtype=torch.bfloat16, device=cuda)
+    y = ops.gemv_fp8(Wq, scale, x, bias=bias)                     # all on the GPU: runs
+    torch.cuda.synchronize()
+    assert y.device == Wq.device and y.shape == (N,)
+    for what, args, kw in [("x", (Wq, scale, x.cpu()), {}), ("scale", (Wq, scale.cpu(), x), {}),
+                           ("bias", (Wq, scale, x), {"bias": bias.cpu()}),
+                           ("out", (Wq, scale, x), {"out": torch.empty(N, dtype=torch.bfloat16)})]:
+        note(f"host {what}")
+        with pytest.raises(RuntimeError, match="device"):
+            ops.gemv_fp8(*args, **kw)
+    Wb = torch.zeros(N, K, dtype=torch.bfloat16)                  # weights on the host, x on the GPU
+    with pytest.raises(RuntimeError):
+        ops.gemv_bf16(Wb, x)
+    torch.cuda.synchronize()
