@@ -10,7 +10,8 @@
 //   paia_gemv_int4_zp       fused kernel, same variant table as paia_gemv_int4
 //
 // Variant knobs on gfx950: R rows per wave {1,2,4,8}, U 16-byte loads per row per batch {1,2,4}, W waves per block
-// {4,8}, H split-K inside the block {0,1}. Weight loads are always "nt" (S reported as 0).
+// {4,8}, H split-K inside the block {0,1}; plus W = 16 (one block per CU) with R {1,2}, U {1,2,4}, H 0. Weight loads
+// are always "nt" (S reported as 0).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -91,14 +92,17 @@ int launch_i4(GemvParams p, hipStream_t st)
 #define QV_W(R, U, H) QV(R, U, 4, H) QV(R, U, 8, H)
 #define QV_H(R, U) QV_W(R, U, 0) QV_W(R, U, 1)
 #define QV_U(R) QV_H(R, 1) QV_H(R, 2) QV_H(R, 4)
-const Variant kInt4Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8)};
+// one 16-wave block per CU (row-parallel only), appended so the indices above stay stable
+#define QV_16 QV(1, 1, 16, 0) QV(1, 2, 16, 0) QV(1, 4, 16, 0) QV(2, 1, 16, 0) QV(2, 2, 16, 0) QV(2, 4, 16, 0)
+const Variant kInt4Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
 #undef QV
 #define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4ZP, R, U, W, H>},
-const Variant kInt4ZpVariants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8)};
+const Variant kInt4ZpVariants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
 #undef QV
 #undef QV_W
 #undef QV_H
 #undef QV_U
+#undef QV_16
 constexpr int kNumInt4 = (int)(sizeof(kInt4Variants) / sizeof(kInt4Variants[0]));
 static_assert(sizeof(kInt4Variants) == sizeof(kInt4ZpVariants), "int4 tables must match");
 

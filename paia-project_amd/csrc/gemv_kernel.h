@@ -380,7 +380,9 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     // x loads first (ahead of the weight loads in the memory queues), then all D item buffers, then x into LDS.
     // All D buffers are in flight while x is staged, so a small GEMV (a few items per wave) costs one memory round
     // trip. From then on, the buffer just consumed is refilled with the item D places further on (D = 2).
-    constexpr int XE = 1024 / (W * kWave);   // early x vectors per thread: 16 KiB of x per block
+    // early x vectors per thread: 16 KiB of x per block, 32 KiB for the one-block-per-CU W = 16 launch (no other
+    // block's weight loads can queue ahead of its x, and K up to 16384 is then staged without late loads)
+    constexpr int XE = (W >= 16 ? 2048 : 1024) / (W * kWave);
     constexpr int D = pipe_depth<R, U>();
     XRegs<XE> xr;
     x_load<F, XE>(p, xr);
@@ -447,11 +449,17 @@ struct DeviceFacts {
 };
 DeviceFacts device_facts();
 
-// Resident waves per CU the persistent grid aims for (each block stages x, so more blocks mean more x traffic).
+// Resident waves per CU the persistent grid aims for (each block stages x, so more blocks mean more x traffic). A
+// 16-wave block runs alone on its CU: staging x once per CU, ahead of every weight load there, is what it is for.
 #ifndef PAIA_GEMV_MAX_WAVES_PER_CU
 #define PAIA_GEMV_MAX_WAVES_PER_CU 32
 #endif
 constexpr int kMaxWavesPerCu = PAIA_GEMV_MAX_WAVES_PER_CU;
+template <int W>
+constexpr int max_blocks_per_cu_for()
+{
+    return W >= 16 ? 1 : (kMaxWavesPerCu / W > 0 ? kMaxWavesPerCu / W : 1);
+}
 
 // Largest LDS a launch may request (bytes). Beyond it the entry points return -2.
 constexpr uint32_t kMaxLds = 65536;
@@ -505,7 +513,7 @@ int launch_gemv(GemvParams p, hipStream_t st)
         const int by_lds = (int)(df.lds_per_cu / (lds ? lds : 1u));
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
     }
-    if (per_cu * W > kMaxWavesPerCu) per_cu = kMaxWavesPerCu / W > 0 ? kMaxWavesPerCu / W : 1;
+    if (per_cu > max_blocks_per_cu_for<W>()) per_cu = max_blocks_per_cu_for<W>();
     const int gmax = (df.cus > 0 ? df.cus : 256) * per_cu;
     // units of work dealt round-robin: row groups to waves (H=0) or to blocks (H=1)
     const int per_block_units = KSPLIT ? 1 : W;

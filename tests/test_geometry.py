@@ -54,6 +54,8 @@ def launch(fmt, N, K, R, U, W, H, cus, per_cu):
     if lds == 0:
         return None
     per_cu = min(per_cu, max(1, (160 * 1024) // lds))
+    if W >= 16:
+        per_cu = 1                   # a 16-wave block runs alone on its CU
     gmax = cus * per_cu
     unit = 1 if H else W
     grid = min(-(-p["ngroups"] // unit), gmax)
@@ -140,6 +142,9 @@ KNOBS = {
     "fp8": list(itertools.product([1, 2, 4], [1, 2, 4], [4, 8], [0, 1])),
     "int4": list(itertools.product([1, 2, 4, 8], [1, 2, 4], [4, 8], [0, 1])),
 }
+W16 = [(R, U, 16, 0) for R in (1, 2) for U in (1, 2, 4)]   # one 16-wave block per CU, row-parallel only
+for _f in ("fp8", "int4"):
+    KNOBS[_f] = KNOBS[_f] + W16
 KNOBS["int4zp"] = KNOBS["int4"]
 SHAPES = {
     "bf16": [(1, 8), (3, 264), (7, 520), (33, 1032), (129, 4104), (257, 3584), (100, 18944), (65, 4096), (17, 14336)],

@@ -44,14 +44,14 @@ def test_variant_tables_hold_harness_defaults(gemv_lib):
     """paia-bench/bench/ops/ours_bf16.py:22 and ours_quant.py:19 look these tuples up by value (KeyError otherwise)."""
     def has(vs, want):
         return any(all(v[k] == want[k] for k in "RUWSH") for v in vs)
-    assert gemv_lib.n_variants == 96 and len(gemv_lib.variants_fp8) == 36 and len(gemv_lib.variants_int4) == 48
+    assert gemv_lib.n_variants == 96 and len(gemv_lib.variants_fp8) == 42 and len(gemv_lib.variants_int4) == 54
     assert has(gemv_lib.variants, {"R": 2, "U": 4, "W": 4, "S": 0, "H": 1})
     assert has(gemv_lib.variants_fp8, {"R": 2, "U": 2, "W": 4, "S": 0, "H": 1})
     assert has(gemv_lib.variants_int4, {"R": 4, "U": 2, "W": 4, "S": 0, "H": 1})
     keys = {(v["R"], v["U"], v["W"], v["S"], v["H"]) for v in gemv_lib.variants}
     assert len(keys) == 96                                               # tuples are unique
     for kind in ("bf16", "fp8", "int4", "int4zp"):
-        n = {"bf16": 96, "fp8": 36, "int4": 48, "int4zp": 48}[kind]
+        n = {"bf16": 96, "fp8": 42, "int4": 54, "int4zp": 54}[kind]
         for N, K in [(4096, 4096), (6144, 4096), (3584, 18944), (1, 128)]:
             assert 0 <= gemv_lib.pick_variant(kind, N, K) < n
 
@@ -75,10 +75,10 @@ def test_contract_return_codes_without_launch(gemv_lib):
     assert L.paia_gemv_bf16(A, A, A, 4, 16, 96, None) == -1           # variant out of range
     assert L.paia_gemv_fp8(A, A, A, A, 4, 24, 0, None) == -2          # K % 16
     assert L.paia_gemv_fp8(A, A + 2, A, A, 4, 32, 0, None) == -2      # scale not 4-byte aligned
-    assert L.paia_gemv_fp8(A, A, A, A, 4, 32, 36, None) == -1
+    assert L.paia_gemv_fp8(A, A, A, A, 4, 32, len(gemv_lib.variants_fp8), None) == -1
     assert L.paia_gemv_int4(A, A, A, A, 4, 64, 0, None) == -2         # K % 128
     assert L.paia_gemv_int4(A, A + 1, A, A, 4, 128, 0, None) == -2    # scales not 2-byte aligned
-    assert L.paia_gemv_int4(A, A, A, A, 4, 128, 48, None) == -1
+    assert L.paia_gemv_int4(A, A, A, A, 4, 128, len(gemv_lib.variants_int4), None) == -1
     assert L.paia_gemv_int4_naive(A, A, A, A, 4, 64, None) == -2
     assert L.paia_gemv_int4_unfused(A, A, A, A, A + 8, 4, 128, None) == -2   # scratch alignment
     assert L.paia_gemv_int4_zp(A, A, None, A, None, A, 4, 128, 0, None) == -2  # zeros missing
