@@ -7,11 +7,13 @@ Workload (the metric's configuration): FP8 W8A16 M=1 GEMVs 
 qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336, OCP e4m3fn weights with a per-row fp32 scale, bf16
 activations and outputs. One step = the four GEMVs of one decoder layer; steps rotate over L distinct layer copies
 whose total (>= 4 x 256 MiB) defeats the Infinity Cache, so every weight byte comes from HBM. The timed region is one
-hipGraph replay of K steps, bracketed by device synchronisation, with all inputs resident in HBM. Each GEMV uses the
-library's per-shape variant (paia_gemv_pick_variant, the frozen MI355X sweep in paia-project_amd/tuned/mi355x.json).
+hipGraph replay of K steps (that graph launched once, untimed, beforehand), bracketed by device synchronisation,
+with all inputs resident in HBM. Each GEMV uses the library's per-shape variant (paia_gemv_pick_variant, the frozen MI355X
+sweep in paia-project_amd/tuned/mi355x.json).
 
 Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmic GB/s of the step, plus
-  per_gemv      us/GEMV, GB/s and % of 8 TB/s for each shape (graph of R back-to-back launches, rotating copies)
+  per_gemv      us/GEMV, GB/s and % of 8 TB/s for each shape (graph of R back-to-back launches rotating over
+                >= 4 x 256 MiB of copies of that shape alone)
   roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time (hipEvents on the launch
                 stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels of known size
@@ -134,7 +136,7 @@ def main(argv=None):
 
     import torch
     from paia_bench.cases import GemvCase
-    from paia_bench.timing import LLC_BYTES, capture, time_per_call_us
+    from paia_bench.timing import LLC_BYTES, capture, plan_rotation, time_per_call_us
     from paia_gemv import load_lib
     from paia_gemv.shapes import LAYER
 
@@ -175,6 +177,12 @@ def main(argv=None):
     g_timed = capture(steps_fn(a.steps), warm=0)
     g_warm.replay()
     torch.cuda.synchronize()
+    # The first launch of an executable graph does one-time per-node setup on MI355X (measured: the first replay of
+    # this 800-launch graph ran 41.8-42.1 us/step, every later one 40.5-40.7, with or without hipGraphUpload). That
+    # setup is not per-step work, so the timed graph is launched once, untimed, before the timed replay: the run
+    # does W + K untimed steps in all (reported as config.timed_graph_primed).
+    g_timed.replay()
+    torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -190,13 +198,22 @@ def main(argv=None):
         f"{value:.0f} GB/s")
     del g_warm, g_timed
 
+    # per-GEMV figures: each shape on its own, rotating over enough copies of that shape alone (>= 4 x 256 MiB), so
+    # the small shapes cannot run out of the Infinity Cache (the layer's L copies of one o_proj are only 84 MB)
+    for c in cases:
+        c.free()
+    torch.cuda.empty_cache()
     per = {}
     for c in cases:
-        t = time_per_call_us(c.call, L)
+        n_rot = plan_rotation(c.footprint())["n_copies"]
+        c.build(n_rot, dev)
+        t = time_per_call_us(c.call, n_rot)
+        c.free()
+        torch.cuda.empty_cache()
         gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
         per[c.name] = {"us": round(t["us"], 3), "gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1),
                        "variant": lib.variants_fp8[c.variant], "kernel": kernel_name(lib, c),
-                       "bytes": c.bytes()["total"], "R": t["R"]}
+                       "bytes": c.bytes()["total"], "R": t["R"], "copies": n_rot}
         log(f"  {c.name}: {t['us']:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s)")
 
     dom = max(cases, key=lambda c: c.bytes()["total"])
@@ -208,9 +225,6 @@ def main(argv=None):
             "kernel": kernel_name(lib, dom), "case": dom.name, "avg_launch_us": dom_us,
             "algorithmic_bytes": dom.bytes()["total"],
             "traffic_detail": traffic}
-    for c in cases:
-        c.free()
-    torch.cuda.empty_cache()
 
     chain = None
     if not a.no_chain:
@@ -237,7 +251,7 @@ def main(argv=None):
                                   "gate_up 28672x4096, down 4096x14336 (BASELINE configs[1])",
                       "layer_copies": L, "rotation_bytes": L * layer_bytes, "step_bytes": step_bytes,
                       "us_per_layer_step": round(ms_per_step * 1e3, 3),
-                      "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1)},
+                      "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1), "timed_graph_primed": True},
            "per_gemv": per, "roofline": roof, "chain": chain, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
     if a.report:
