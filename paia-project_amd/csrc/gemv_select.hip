@@ -1,13 +1,17 @@
 // Per-shape variant choice for gfx950 (used when a caller passes variant = -1 to the torch ops).
 // No reference C symbol: the reference picks variants in Python from src/tuned/<platform>.json
 // (paia-bench/bench/ops/ours_bf16.py:32-38, ours_quant.py:29-36); this is the same idea compiled into the library so
-// the torch ops need no JSON. Shapes without an entry use the harness default tuples (ours_bf16.py:22,
-// ours_quant.py:19).
+// the torch ops need no JSON. A shape without an entry takes the entry of the nearest tuned shape of its format
+// (smallest |log2(N/N')| + |log2(K/K')|), and only a format with no entry at all the harness default tuples
+// (ours_bf16.py:22, ours_quant.py:19): measured on MI355X, the split-K default runs large untuned shapes ~15% slower
+// than their tuned neighbours' choice (BF16 131072x4096: 74.6% of 8 TB/s, against 90.8% for the tuned 128256x4096).
 //
 // The table is data, not code: paia-project_amd/tuned/mi355x.json keeps the reference's tuned-file schema
 // ("shapes" / "fp8_shapes" / "int4_shapes" keyed "NxK", plus "int4zp_shapes"), written by paia_bench.sweep
 // --write-tuned on an MI355X; build.py turns it into gemv_tuned.inc.
 #include <hip/hip_runtime.h>
+
+#include <cmath>
 
 #include "paia_gemv.h"
 
@@ -54,13 +58,33 @@ int paia_gemv_pick_variant(int kind, int N, int K)
 {
     if (kind < 0 || kind > 3) kind = 0;
     const int table = kind == 3 ? 2 : kind;   // both INT4 formats use the paia_gemv_int4 variant table
+    auto resolve = [&](const Pick& p) {
+        return table == 0 ? find_bf16(p.R, p.U, p.W, p.S, p.H) : find_quant(table, p.R, p.U, p.W, p.H);
+    };
     for (int pass = 0; pass < 2; ++pass) {    // this kind's row first; the asymmetric INT4 falls back to INT4's
         const int want = pass == 0 ? kind : (kind == 3 ? 2 : -2);
         for (const Pick& p : kTuned) {
             if (p.kind == want && p.N == N && p.K == K) {
-                const int v = table == 0 ? find_bf16(p.R, p.U, p.W, p.S, p.H) : find_quant(table, p.R, p.U, p.W, p.H);
+                const int v = resolve(p);
                 if (v >= 0) return v;
             }
+        }
+    }
+    if (N > 0 && K > 0) {
+        for (int pass = 0; pass < 2; ++pass) {
+            const int want = pass == 0 ? kind : (kind == 3 ? 2 : -2);
+            int best = -1;
+            double best_d = 0.0;
+            for (const Pick& p : kTuned) {
+                if (p.kind != want || p.N <= 0 || p.K <= 0) continue;
+                const double d = std::fabs(std::log2((double)N / p.N)) + std::fabs(std::log2((double)K / p.K));
+                const int v = resolve(p);
+                if (v >= 0 && (best < 0 || d < best_d)) {
+                    best = v;
+                    best_d = d;
+                }
+            }
+            if (best >= 0) return best;
         }
     }
     int v = -1;

@@ -7,6 +7,8 @@ graph timing and rotation, keep the best and the top five), same tuned-table sch
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --out gpurun_out/sweep_fp8.json
     python -m paia_bench.sweep --fmt int4zp --shapes baseline --write-tuned paia-project_amd/tuned/mi355x.json
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --batch 1,2,4,8,16     # small-batch kernels (P,U,W,S)
+    python -m paia_bench.sweep --fmt fp8 --shapes frozen --candidates tuned --write-tuned paia-project_amd/tuned/mi355x.json
+        (every other shape of the reference's frozen set, each timed with the variants that won a tuned shape)
 
 Copy 0 of each shape is checked against the CPU fp32 reference (sampled rows) for every variant before it is timed.
 """
@@ -20,7 +22,7 @@ from pathlib import Path
 
 import numpy as np
 
-from paia_gemv.shapes import LAYER, LM_HEAD, MODELS
+from paia_gemv.shapes import LAYER, LM_HEAD, MODELS, SYNTHETIC
 
 from .cases import GemvCase, kind_of
 from .timing import HBM_PEAK_GBPS, plan_rotation, time_per_call_us
@@ -39,6 +41,14 @@ def shape_set(name: str, fmt: str):
     if name in ("real", "all"):
         for m, shp in MODELS.items():
             out += [(f"{m}:{nm}", N, K) for nm, (N, K) in shp.items() if nm != "lm_head"]
+    if name == "frozen":
+        # the reference harness's frozen set (paia-bench/configs/shapes.yaml) minus the BASELINE shapes, which the
+        # full sweep covers (a Qwen qkv entry there is timed with its bias)
+        base = {(N, K) for _, N, K in shape_set("baseline", fmt)}
+        for nm, (K, Ns) in SYNTHETIC.items():
+            out += [(f"synthetic:{nm}_N{N}", N, K) for N in Ns if (N, K) not in base]
+        for m, shp in MODELS.items():
+            out += [(f"{m}:{nm}", N, K) for nm, (N, K) in shp.items() if (N, K) not in base]
     seen, uniq = set(), []
     for nm, N, K in out:
         if K % kmult == 0 and (N, K) not in seen:
@@ -66,8 +76,10 @@ def main(argv=None):
 
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--fmt", choices=["bf16", "fp8", "int4", "int4zp"], required=True)
-    ap.add_argument("--shapes", default="baseline", help="baseline | real | all | NxK[,NxK...]")
+    ap.add_argument("--shapes", default="baseline", help="baseline | real | all | frozen | NxK[,NxK...]")
     ap.add_argument("--variants", default="", help="filter, e.g. 'R=2,U>=2,H=0'")
+    ap.add_argument("--candidates", default="", help="'tuned': only the variants that are some shape's choice in "
+                    "the tuned table (paia-project_amd/tuned/mi355x.json), plus the harness default")
     ap.add_argument("--target-ms", type=float, default=2.0)
     ap.add_argument("--samples", type=int, default=9)
     ap.add_argument("--out", default=None)
@@ -86,10 +98,20 @@ def main(argv=None):
         fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(a.fmt, lib.variants_int4)
         knobs = "RUWSH"
     keep = parse_filter(a.variants)
-    if a.shapes in ("baseline", "real", "all"):
+    if a.candidates == "tuned" and not batch:
+        sec = TKEY[a.fmt] if a.fmt != "int4zp" else "int4zp_shapes"
+        table = json.loads((Path(__file__).resolve().parent.parent / "tuned" / "mi355x.json").read_text())
+        won = {tuple(e["variant"][k] for k in knobs) for e in table.get(sec, {}).values()}
+        won.add({"bf16": (2, 4, 4, 0, 1), "fp8": (2, 2, 4, 0, 1)}.get(a.fmt, (4, 2, 4, 0, 1)))   # harness default
+        filt = keep
+        keep = lambda v: filt(v) and tuple(v[k] for k in knobs) in won
+        have = set(table.get(sec, {}))         # shapes with a full-sweep entry keep it
+    if a.shapes in ("baseline", "real", "all", "frozen"):
         shapes = shape_set(a.shapes, a.fmt)
     else:
         shapes = [(s, *map(int, s.split("x"))) for s in a.shapes.split(",")]
+    if a.candidates == "tuned" and not batch:
+        shapes = [(nm, N, K) for nm, N, K in shapes if f"{N}x{K}" not in have]
     cells = [(nm, N, K, M) for nm, N, K in shapes for M in (batch or [1])]
     results = {}
     for nm, N, K, M in cells:

@@ -17,6 +17,14 @@ QWEN25_7B = {
     "qkv_fused": (4608, 3584), "gate_up_fused": (37888, 3584), "lm_head": (152064, 3584),
 }
 MODELS = {"llama31_8b": LLAMA31_8B, "qwen25_7b": QWEN25_7B}
+
+# The reference harness's frozen synthetic sweep (paia-bench/configs/shapes.yaml:51-60): BF16 weight bytes from
+# 0.25 MiB to 1 GiB in geometric steps at K = 4096 and K = 14336; and its batch sweep M values (:62-64).
+SYNTHETIC = {
+    "K4096": (4096, [32, 64, 128, 256, 384, 768, 1536, 2816, 5376, 10112, 19200, 36480, 69120, 131072]),
+    "K14336": (14336, [32, 64, 128, 256, 384, 768, 1536, 2944, 5504, 10368, 19712, 37504]),
+}
+BATCH_M = [1, 2, 4, 8, 16]
 N_LAYERS = {"llama31_8b": 32, "qwen25_7b": 28}
 
 # The per-layer linear chain of the BASELINE configs: (name, N, K).

@@ -162,3 +162,21 @@ def test_byte_accounting_matches_baseline_table():
     assert gemv_bytes("fp8", 4608, 3584, bias=True)["total"] == 16_559_104
     assert gemv_bytes("int4zp", 3584, 18944)["total"] == 35_318_784
     assert gemv_bytes("bf16", 152064, 3584)["total"] == 1_090_306_048
+
+
+def test_untuned_shapes_take_the_nearest_tuned_entry(gemv_lib):
+    """A shape without a tuned entry gets the choice of the nearest tuned shape of its format (log-distance in N and
+    K), not the split-K harness default; exact entries are unchanged."""
+    L = gemv_lib
+    assert L.pick_variant("bf16", 131072, 4096) == L.pick_variant("bf16", 128256, 4096)
+    assert L.pick_variant("fp8", 28000, 4096) == L.pick_variant("fp8", 28672, 4096)
+    assert L.pick_variant("int4zp", 4096, 14000) == L.pick_variant("int4zp", 4096, 14336)
+    import json
+    tuned = json.loads((ROOT / "paia-project_amd" / "tuned" / "mi355x.json").read_text())
+    want = tuned["fp8_shapes"]["28672x4096"]["variant"]                                     # exact entries stand
+    got = L.variants_fp8[L.pick_variant("fp8", 28672, 4096)]
+    assert all(got[k] == want[k] for k in "RUWH")
+    for kind in ("bf16", "fp8", "int4", "int4zp"):
+        n = {"bf16": L.n_variants, "fp8": len(L.variants_fp8)}.get(kind, len(L.variants_int4))
+        for N, K in [(32, 4096), (300000, 4096), (1000, 30720), (8192, 8192)]:
+            assert 0 <= L.pick_variant(kind, N, K) < n
