@@ -9,10 +9,15 @@
 // Variant knobs: P tiles of 16 rows per wave, U k-blocks (128 columns) of loads in flight per wave, W waves per block,
 // S waves sharing a tile along K (split-K inside the block), X how x reaches the matrix cores (0 staged in LDS per
 // K-chunk, 1 loaded with the weights). variant < 0 selects paia_gemv_batch_pick_variant's.
+//
+// P = 0 marks the row-streaming kernel instead (gemv_rows_kernel: the M = 1 GEMV's weight stream and decode with one
+// accumulator per activation row, for M = 2..4): then U is its 1-KiB chunks per item, W its waves per block, S its
+// weight rows per wave (R) and X the one M it serves (other M: -2). These entries follow the matrix-core ones.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "gemv_batch.h"
+#include "gemv_kernel.h"
 #include "paia_gemv.h"
 
 namespace {
@@ -24,22 +29,49 @@ int launch_b(BatchParams p, hipStream_t st)
     return launch_batch<F, P, U, W, X>(p, st);
 }
 
+// the row-streaming kernel for exactly MB activation rows (weights streamed once: nt loads)
+template <int F, int R, int U, int W, int MB>
+int launch_rows_b(BatchParams b, hipStream_t st)
+{
+    if (b.M != MB) return -2;
+    GemvParams p{};
+    p.W = b.W;
+    p.meta = b.meta;
+    p.zeros = b.zeros;
+    p.x = b.x;
+    p.bias = b.bias;
+    p.y = b.y;
+    p.N = b.N;
+    p.K = b.K;
+    p.row_bytes = b.row_bytes;
+    p.meta_bytes = b.meta_bytes;
+    p.zbytes = b.zbytes;
+    return launch_gemv_rows<F, R, U, W, 2, MB>(p, st);
+}
+
 #define BV(F, P, U, W, S, X) {P, U, W, S, X, &launch_b<F, P, U, W, X>},
+#define RV(F, R, U, W, MB) {0, U, W, R, MB, &launch_rows_b<F, R, U, W, MB>},
+#define RV_M(F, R, U, W) RV(F, R, U, W, 2) RV(F, R, U, W, 3) RV(F, R, U, W, 4)
+#define RV_ALL(F) RV_M(F, 1, 2, 8) RV_M(F, 2, 2, 4) RV_M(F, 1, 1, 8) RV_M(F, 2, 1, 4) RV_M(F, 1, 2, 16) \
+                  RV_M(F, 2, 1, 16)
 #define BV_S(F, P, U, X) BV(F, P, U, 4, 1, X) BV(F, P, U, 4, 2, X) BV(F, P, U, 4, 4, X) \
                          BV(F, P, U, 8, 1, X) BV(F, P, U, 8, 2, X) BV(F, P, U, 8, 4, X) BV(F, P, U, 8, 8, X)
 #define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1)
 // register budget: P * U * (16-byte loads per k-block) <= 16 buffers of 4 VGPRs (INT4 P=2 U=8 with x loaded
 // alongside spilled, so it is left out)
-const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2)};
+const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2) RV_ALL(kBF16)};
 const BatchVariant kFp8Batch[] = {BV_W(kFP8, 1, 2) BV_W(kFP8, 1, 4) BV_W(kFP8, 1, 8) BV_W(kFP8, 2, 2)
-                                      BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2)};
+                                      BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2) RV_ALL(kFP8)};
 const BatchVariant kI4Batch[] = {BV_W(kI4, 1, 4) BV_W(kI4, 1, 8) BV_W(kI4, 2, 2) BV_W(kI4, 2, 4) BV_W(kI4, 4, 2)
-                                     BV_W(kI4, 4, 4)};
+                                     BV_W(kI4, 4, 4) RV_ALL(kI4)};
 const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4ZP, 2, 2) BV_W(kI4ZP, 2, 4)
-                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4)};
+                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4) RV_ALL(kI4ZP)};
 #undef BV
 #undef BV_S
 #undef BV_W
+#undef RV
+#undef RV_M
+#undef RV_ALL
 
 struct Table {
     const BatchVariant* v;
@@ -63,13 +95,17 @@ int find(const Table& t, int P, int U, int W, int S, int X)
     return -1;
 }
 
-// Whether variant v can run (M, K): X=0 needs a chunk of U k-blocks of x for all S splits in LDS.
+// Whether variant v can run (M, K): X=0 needs a chunk of U k-blocks of x for all S splits in LDS; a row-streaming
+// variant serves its own M only (its LDS limit is checked at launch).
 bool fits(const BatchVariant& v, int M)
 {
+    if (v.P == 0) return v.X == M;
     return v.X == 1 || batch_x_bytes(v.S, M, v.U) <= kBatchLds;
 }
 
-// Default choice, fitted to MI355X sweeps of the Llama/Qwen projection shapes at M = 1, 4, 16 (FP8 and INT4):
+// Default choice: a measured entry for the shape and M when the tuned table has one; otherwise a rule fitted to MI355X
+// sweeps of the Llama/Qwen projection shapes (FP8 and INT4). M = 2..4 take the row-streaming kernel when its x copies
+// fit the LDS (pick_rows); otherwise the matrix-core kernel:
 //   * split-K S: at least two splits (every shape streamed faster with two waves per tile than with one), then the
 //     fewest (<= 8, >= 2 k-blocks each) that give >= 1152 work units (tiles x splits, 4.5 per CU): qkv (384 tiles)
 //     measured best at S = 4, o/down (256 tiles) at S = 8, gate_up (1792 tiles) at S = 2;
@@ -87,10 +123,54 @@ int pick_splits(int units0, int KB, int W)
     return S;
 }
 
+// LDS of the row-streaming kernel at M activation rows: M staged copies of x (+ INT4 lane sums).
+uint64_t rows_lds(int kind, int M, int K)
+{
+    const uint64_t row_bytes = kind == 0 ? 2ull * K : (kind == 1 ? (uint64_t)K : (uint64_t)K / 2);
+    const uint64_t nchunks = (row_bytes + kChunkBytes - 1) / kChunkBytes;
+    const uint64_t xq = kind == 0 ? 1 : (kind == 1 ? 2 : 4);
+    return (uint64_t)M * nchunks * (xq * kChunkBytes + (kind >= 2 ? kWave * 4u : 0u));
+}
+
+// The row-streaming variant for M = 2..4: the M = 1 tuned choice's (R, U, W) when the table has that triple (the
+// weight stream is the M = 1 kernel's), else R=1 U=2 W=8. -1 when its x copies do not fit the LDS.
+int pick_rows(const Table& t, int kind, int M, int N, int K)
+{
+    if (M < 2 || M > 4 || rows_lds(kind, M, K) > kMaxLds) return -1;
+    int R = 1, U = 2, W = 8;
+    const int v1 = paia_gemv_pick_variant(kind, N, K);
+    int r = 0, u = 0, w = 0, s = 0, h = 1;
+    const int rc = kind == 0 ? paia_gemv_bf16_variant_info(v1, &r, &u, &w, &s, &h)
+                             : (kind == 1 ? paia_gemv_fp8_variant_info(v1, &r, &u, &w, &h)
+                                          : paia_gemv_int4_variant_info(v1, &r, &u, &w, &h));
+    if (rc == 0 && h == 0 && find(t, 0, u, w, r, M) >= 0) {
+        R = r;
+        U = u;
+        W = w;
+    }
+    return find(t, 0, U, W, R, M);
+}
+
+// Measured choices for the BASELINE shapes (tuned/mi355x.json's "*batch_shapes" sections, compiled in by build.py).
+struct BatchPick {
+    int kind, M, N, K, P, U, W, S, X;
+};
+const BatchPick kBatchTuned[] = {
+#include "gemv_batch_tuned.inc"
+    {-1, 0, 0, 0, 0, 0, 0, 0, 0},   // end marker
+};
+
 int pick(int kind, int M, int N, int K)
 {
     const Table t = table(kind);
     if (!t.v || M < 1 || M > kMaxBatch || N <= 0 || K <= 0) return -1;
+    for (const BatchPick& b : kBatchTuned)
+        if (b.kind == kind && b.M == M && b.N == N && b.K == K) {
+            const int v = find(t, b.P, b.U, b.W, b.S, b.X);
+            if (v >= 0 && fits(t.v[v], M)) return v;
+        }
+    const int rv = pick_rows(t, kind, M, N, K);
+    if (rv >= 0) return rv;
     const int W = 8;
     const int ntiles = (N + kTileRows - 1) / kTileRows;
     const int KB = (K + kBlockCols - 1) / kBlockCols;

@@ -140,6 +140,17 @@ __device__ __forceinline__ float i4_word_dot(uint32_t w, const u32x4 x, float ac
     acc = dot2_bf16(__builtin_amdgcn_perm(c43, hi, 0x04030402u), x.w, acc);   // (128+q5, 128+q7)
     return acc;
 }
+// The same decode without the products: the four bf16 pairs (128 + q) of one word, in i4_word_dot's order, for
+// callers that take several dot products per decoded word (one per activation row).
+__device__ __forceinline__ void i4_word_decode(uint32_t w, uint32_t c43, uint32_t q4[4])
+{
+    const uint32_t lo = w & 0x0F0F0F0Fu;
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    q4[0] = __builtin_amdgcn_perm(c43, lo, 0x04010400u);
+    q4[1] = __builtin_amdgcn_perm(c43, lo, 0x04030402u);
+    q4[2] = __builtin_amdgcn_perm(c43, hi, 0x04010400u);
+    q4[3] = __builtin_amdgcn_perm(c43, hi, 0x04030402u);
+}
 __device__ __forceinline__ float dot_i4_16B(const u32x4 w, const u32x4 x0, const u32x4 x1, const u32x4 x2,
                                             const u32x4 x3, uint32_t c43)
 {

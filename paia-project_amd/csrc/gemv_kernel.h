@@ -81,12 +81,13 @@ struct XRegs {
     u32x4 v[XE];
 };
 
-template <int F, int XE>
-__device__ __forceinline__ void x_load(const GemvParams& p, XRegs<XE>& xr)
+// NT: threads per block (a compile-time constant, so no work-group size read from the dispatch packet).
+template <int F, int XE, int NT>
+__device__ __forceinline__ void x_load(const uint16_t* x, int K, XRegs<XE>& xr)
 {
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)p.K * 2u);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)K * 2u);
 #pragma unroll
-    for (int e = 0; e < XE; ++e) xr.v[e] = ld16<0>(xrs, ((uint32_t)threadIdx.x + (uint32_t)(e * blockDim.x)) * 16u, 0u);
+    for (int e = 0; e < XE; ++e) xr.v[e] = ld16<0>(xrs, ((uint32_t)threadIdx.x + (uint32_t)(e * NT)) * 16u, 0u);
 }
 
 template <int F>
@@ -113,20 +114,21 @@ __device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
     xs[(c * XQ + j) * kWave + l] = v;
 }
 
-// Store the XE early vectors, then load+store the rest. nq and blockDim are multiples of 4, so the `q < nq` tests are
+// Store the XE early vectors, then load+store the rest. nq and NT are multiples of 4, so the `q < nq` tests are
 // uniform over each quad (quad_sum needs the whole quad).
-template <int F, int XE>
-__device__ __forceinline__ void x_store(const GemvParams& p, const XRegs<XE>& xr, u32x4* xs, float* s32)
+template <int F, int XE, int NT>
+__device__ __forceinline__ void x_store(const uint16_t* x, int K, int nchunks, const XRegs<XE>& xr, u32x4* xs,
+                                        float* s32)
 {
     constexpr int XQ = FmtInfo<F>::kXQ;
-    const int nq = p.nchunks * XQ * kWave;
-    const int T = (int)blockDim.x;
+    const int nq = nchunks * XQ * kWave;
+    constexpr int T = NT;
 #pragma unroll
     for (int e = 0; e < XE; ++e) {
         const int q = (int)threadIdx.x + e * T;
         if (q < nq) x_put<F>(q, xr.v[e], xs, s32);
     }
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, (uint32_t)p.K * 2u);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)K * 2u);
     for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
 }
 
@@ -173,15 +175,21 @@ struct ItemWalker {
     }
 };
 
-template <int F, int R, int U, int W, int AUX, bool KSPLIT>
-__global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
+// The kernel body. MB activation rows (x [MB][K], y [MB][N]): MB = 1 is the M = 1 GEMV (gemv_kernel); MB = 2..4 is
+// the row-streaming small-batch kernel (gemv_rows_kernel): the same weight stream and decode, with MB accumulators
+// per row and MB staged copies of x, so each weight is loaded and decoded once for all activation rows.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB>
+__device__ __forceinline__ void gemv_body(const GemvParams& p)
 {
+    static_assert(MB >= 1 && MB <= 4 && (MB == 1 || !KSPLIT), "activation rows: 1..4, split-K only at M = 1");
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, then (H=1) the split-K partials
+    const uint32_t xrow = lds_x_bytes<F>(p.nchunks), srow = lds_s32_bytes<F>(p.nchunks);
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
-    float* s32 = reinterpret_cast<float*>(smem + lds_x_bytes<F>(p.nchunks));
-    float* part = reinterpret_cast<float*>(smem + lds_x_bytes<F>(p.nchunks) + lds_s32_bytes<F>(p.nchunks));
+    float* s32 = reinterpret_cast<float*>(smem + MB * xrow);
+    float* part = reinterpret_cast<float*>(smem + MB * xrow + MB * srow);
 
     const int lane = lane_id();
     const int wave = wave_id();
@@ -283,10 +291,91 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    float accm[R][MB];   // MB > 1: one accumulator per (row, activation row)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) accm[r][m] = 0.0f;
+    const int xstride = (int)(xrow / 16u);                   // u32x4 per staged x copy
+    const int sstride = (int)(srow / 4u);                    // floats per staged lane-sum copy
 
     // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
     // staged chunk so every product stays 0 * finite.
+    auto consume_rows = [&](const Item<F, R, U>& B) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            int c = B.chunk0 + u;
+            c = c < nchunks ? c : nchunks - 1;
+            u32x4 xv[MB][XQ];
+#pragma unroll
+            for (int m = 0; m < MB; ++m)
+#pragma unroll
+                for (int j = 0; j < XQ; ++j) xv[m][j] = xs[m * xstride + (c * XQ + j) * kWave + lane];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const u32x4 w = B.w[r][u];
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+                if constexpr (F == kBF16) {
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) accm[r][m] = dot_bf16_16B(w, xv[m][0], accm[r][m]);
+                } else if constexpr (F == kFP8) {
+                    // decode the 16 weights once (8 bf16 pairs), then one v_dot2 chain per activation row
+                    uint32_t d[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        d[2 * i] = fp8x2_to_bf16x2<false>(ww[i]);
+                        d[2 * i + 1] = fp8x2_to_bf16x2<true>(ww[i]);
+                    }
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        const uint32_t xa[8] = {xv[m][0].x, xv[m][0].y, xv[m][0].z, xv[m][0].w,
+                                                xv[m][1].x, xv[m][1].y, xv[m][1].z, xv[m][1].w};
+                        float a = accm[r][m];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) a = dot2_bf16(d[i], xa[i], a);
+                        accm[r][m] = a;
+                    }
+                } else {
+                    float dm[MB];
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) dm[m] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {   // word i: 8 nibbles -> 4 bf16 pairs (128 + q), then MB dot chains
+                        uint32_t q4[4];
+                        i4_word_decode(ww[i], c43, q4);
+#pragma unroll
+                        for (int m = 0; m < MB; ++m) {
+                            const u32x4 xw = xv[m][i];
+                            dm[m] = dot2_bf16(q4[0], xw.x, dm[m]);
+                            dm[m] = dot2_bf16(q4[1], xw.y, dm[m]);
+                            dm[m] = dot2_bf16(q4[2], xw.z, dm[m]);
+                            dm[m] = dot2_bf16(q4[3], xw.w, dm[m]);
+                        }
+                    }
+                    float s, zc;
+                    if constexpr (F == kI4) {
+                        s = f16_to_f32(B.s[r][u]);
+                        zc = 136.0f;                              // 128 (magic) + 8 (zero point)
+                    } else {
+                        s = bf16_to_f32(B.s[r][u]);
+                        const uint32_t z = (B.z[r][u] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu;
+                        zc = 128.0f + (float)z;
+                    }
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        const float sx = s32[m * sstride + c * kWave + lane];
+                        accm[r][m] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, dm[m]), accm[r][m]);
+                    }
+                }
+            }
+        }
+    };
+
     auto consume = [&](const Item<F, R, U>& B) {
+        if constexpr (MB > 1) {
+            consume_rows(B);
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int c = B.chunk0 + u;
@@ -321,7 +410,45 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     };
 
     // End of a group for this wave: reduce over the wave, then store (H=0) or park the partial in LDS (H=1).
+    // MB > 1: reduce the R x MB sums (two per paired wave reduction), then lanes kk*R + r store row r's MB outputs
+    auto finish_rows = [&](const Item<F, R, U>& B) {
+        constexpr int NV = R * MB;
+        float flat[NV], tot[NV];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                flat[r * MB + m] = accm[r][m];
+                accm[r][m] = 0.0f;
+            }
+#pragma unroll
+        for (int i = 0; i + 1 < NV; i += 2) {
+            const float v = wave_sum2(flat[i], flat[i + 1]);
+            tot[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+            tot[i + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+        }
+        if constexpr (NV & 1) tot[NV - 1] = wave_sum(flat[NV - 1]);
+        const int kk = B.k;
+        const int r = lane - kk * R;
+        const int row = B.group * R + r;
+        if (r >= 0 && r < R && row < p.N) {
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                float v = tot[m];
+#pragma unroll
+                for (int i = 1; i < R; ++i) v = r == i ? tot[i * MB + m] : v;
+                if constexpr (F == kFP8) v = v * __uint_as_float(ep_scale);
+                if (p.bias) v = v + bf16_to_f32(ep_bias);
+                p.y[(size_t)m * (size_t)p.N + row] = (uint16_t)f32_to_bf16_out(v);
+            }
+        }
+    };
+
     auto finish = [&](const Item<F, R, U>& B) {
+        if constexpr (MB > 1) {
+            finish_rows(B);
+            return;
+        }
         float tot[R];
 #pragma unroll
         for (int r = 0; r + 1 < R; r += 2) {
@@ -382,15 +509,21 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     // trip. From then on, the buffer just consumed is refilled with the item D places further on (D = 2).
     // early x vectors per thread: 16 KiB of x per block, 32 KiB for the one-block-per-CU W = 16 launch (no other
     // block's weight loads can queue ahead of its x, and K up to 16384 is then staged without late loads)
-    constexpr int XE = (W >= 16 ? 2048 : 1024) / (W * kWave);
+    // (MB > 1: the same early budget shared over the MB activation rows, at least one vector per thread each)
+    constexpr int XE0 = (W >= 16 ? 2048 : 1024) / (W * kWave);
+    constexpr int XE = MB == 1 ? XE0 : (XE0 / MB > 0 ? XE0 / MB : 1);
     constexpr int D = pipe_depth<R, U>();
-    XRegs<XE> xr;
-    x_load<F, XE>(p, xr);
+    XRegs<XE> xr[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) x_load<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, xr[m]);
     if constexpr (!KSPLIT) ep_load(0);
     Item<F, R, U> buf[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(buf[d]);
-    x_store<F, XE>(p, xr, xs, s32);
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+        x_store<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xr[m], xs + m * xstride,
+                                  s32 + m * sstride);
     __syncthreads();
 
     // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
@@ -438,6 +571,19 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     }
 }
 
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+__global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, KSPLIT, 1>(p);
+}
+
+// Small batch on the M = 1 design: MB = 2..4 activation rows, row-parallel (no split-K).
+template <int F, int R, int U, int W, int AUX, int MB>
+__global__ void __launch_bounds__(W * kWave) gemv_rows_kernel(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, false, MB>(p);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------------------------------
@@ -482,33 +628,34 @@ uint32_t gemv_lds_plan(int nchunks, int* round)
     return base + part;
 }
 
-template <int F, int R, int U, int W, int AUX, bool KSPLIT>
-int gemv_max_blocks_per_cu()
+// Resident blocks per CU the occupancy calculator allows for a kernel (queried once per kernel).
+template <typename KernelT>
+int max_blocks_per_cu_of(KernelT kernel, int threads, std::atomic<int>& cached)
 {
-    static std::atomic<int> cached{0};
     int v = cached.load(std::memory_order_relaxed);
     if (v == 0) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<F, R, U, W, AUX, KSPLIT>, W * kWave, 0) !=
-                hipSuccess || n <= 0)
-            n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n <= 0) n = 1;
         cached.store(n, std::memory_order_relaxed);
         v = n;
     }
     return v;
 }
 
-// Launch on `st`. Arguments were validated by the caller. Returns 0, -2 (LDS limit), or a hipError_t.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
-int launch_gemv(GemvParams p, hipStream_t st)
+int gemv_max_blocks_per_cu()
 {
-    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
-    p.nseg = (p.nchunks + U - 1) / U;
-    p.ngroups = (p.N + R - 1) / R;
-    const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
-    if (lds == 0) return -2;
+    static std::atomic<int> cached{0};
+    return max_blocks_per_cu_of(gemv_kernel<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
+}
+
+// Persistent grid of a launch: blocks resident at once (occupancy, LDS, the waves-per-CU cap), then the groups per
+// wave (H=0) or per block (H=1) that cover N, at most 64/R per wave for H=0 so a wave's epilogue operands fit one
+// register (beyond that the grid grows past one resident wave of blocks).
+template <int R, int W, bool KSPLIT>
+int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
+{
     const DeviceFacts df = device_facts();
-    int per_cu = gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>();
     if (df.lds_per_cu > 0) {
         const int by_lds = (int)(df.lds_per_cu / (lds ? lds : 1u));
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
@@ -520,11 +667,39 @@ int launch_gemv(GemvParams p, hipStream_t st)
     int grid = (p.ngroups + per_block_units - 1) / per_block_units;
     if (grid > gmax) grid = gmax;
     int q = (p.ngroups + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
-    // H=0: at most 64/R row groups per wave, so the wave's epilogue operands fit one register (beyond that the
-    // grid grows past one resident wave of blocks)
     if (!KSPLIT && q > kWave / R) q = kWave / R;
-    grid = (p.ngroups + q * per_block_units - 1) / (q * per_block_units);
+    return (p.ngroups + q * per_block_units - 1) / (q * per_block_units);
+}
+
+// Launch on `st`. Arguments were validated by the caller. Returns 0, -2 (LDS limit), or a hipError_t.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+int launch_gemv(GemvParams p, hipStream_t st)
+{
+    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
+    p.nseg = (p.nchunks + U - 1) / U;
+    p.ngroups = (p.N + R - 1) / R;
+    const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
+    if (lds == 0) return -2;
+    const int grid = gemv_grid<R, W, KSPLIT>(p, lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>());
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
+    return (int)hipGetLastError();
+}
+
+// The row-streaming small-batch launch: MB activation rows (x [MB][K], y [MB][N]); LDS holds MB copies of the
+// staged x (and INT4 lane sums). Returns -2 when they exceed kMaxLds.
+template <int F, int R, int U, int W, int AUX, int MB>
+int launch_gemv_rows(GemvParams p, hipStream_t st)
+{
+    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
+    p.nseg = (p.nchunks + U - 1) / U;
+    p.ngroups = (p.N + R - 1) / R;
+    p.round = 1;
+    const uint64_t lds = (uint64_t)MB * (lds_x_bytes<F>(p.nchunks) + lds_s32_bytes<F>(p.nchunks));
+    if (lds > kMaxLds) return -2;
+    static std::atomic<int> cached{0};
+    const int per_cu = max_blocks_per_cu_of(gemv_rows_kernel<F, R, U, W, AUX, MB>, W * kWave, cached);
+    const int grid = gemv_grid<R, W, false>(p, (uint32_t)lds, per_cu);
+    hipLaunchKernelGGL((gemv_rows_kernel<F, R, U, W, AUX, MB>), dim3(grid), dim3(W * kWave), (uint32_t)lds, st, p);
     return (int)hipGetLastError();
 }
 

@@ -9,6 +9,8 @@ graph timing and rotation, keep the best and the top five), same tuned-table sch
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --batch 1,2,4,8,16     # small-batch kernels (P,U,W,S)
     python -m paia_bench.sweep --fmt fp8 --shapes frozen --candidates tuned --write-tuned paia-project_amd/tuned/mi355x.json
         (every other shape of the reference's frozen set, each timed with the variants that won a tuned shape)
+    python -m paia_bench.sweep --fmt fp8 --merge rows.json mfma.json --write-tuned paia-project_amd/tuned/mi355x.json
+        (small batch: the fastest measured variant per "MxNxK" over several sweeps' --out files)
 
 Copy 0 of each shape is checked against the CPU fp32 reference (sampled rows) for every variant before it is timed.
 """
@@ -86,7 +88,19 @@ def main(argv=None):
     ap.add_argument("--write-tuned", default=None)
     ap.add_argument("--batch", default="", help="M values: time the small-batch kernels (variants P,U,W,S,X)")
     ap.add_argument("--pick-only", action="store_true", help="time only the library's choice for each cell")
+    ap.add_argument("--merge", nargs="+", default=None,
+                    help="no timing: merge these --out files (fastest per cell) into --write-tuned")
     a = ap.parse_args(argv)
+    if a.merge:
+        if not a.write_tuned:
+            raise SystemExit("--merge needs --write-tuned")
+        merged = {}
+        for fn in a.merge:
+            for key, r in json.loads(Path(fn).read_text())["results"].items():
+                if r["ranked"] and (key not in merged or r["ranked"][0]["us"] < merged[key]["ranked"][0]["us"]):
+                    merged[key] = r
+        write_tuned(Path(a.write_tuned), a.fmt, merged)
+        return 0
 
     lib = load_lib()
     dev = torch.device("cuda:0")
@@ -164,23 +178,29 @@ def main(argv=None):
     if a.out:
         Path(a.out).parent.mkdir(parents=True, exist_ok=True)
         Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
-    if a.write_tuned and batch:
-        raise SystemExit("--write-tuned is for the M = 1 tables")
     if a.write_tuned:
-        f = Path(a.write_tuned)
-        tuned = json.loads(f.read_text()) if f.exists() else {"platform": "mi355x", "shapes": {}}
-        sec = tuned.setdefault(TKEY[a.fmt] if a.fmt != "int4zp" else "int4zp_shapes", {})
-        for key, r in results.items():
-            if not r["ranked"]:
-                continue
-            best = r["ranked"][0]
-            sec[key] = {"variant": best["variant"], "us": best["us"], "gbps": best["gbps"],
-                        "top5": [{"variant": x["variant"], "pct_of_best": 100 * best["us"] / x["us"]}
-                                 for x in r["ranked"][:5]],
-                        "when": time.strftime("%Y-%m-%d %H:%M")}
-        f.parent.mkdir(parents=True, exist_ok=True)
-        f.write_text(json.dumps(tuned, indent=1))
+        write_tuned(Path(a.write_tuned), a.fmt, results)
     return 0
+
+
+def write_tuned(f: Path, fmt: str, results: dict):
+    """Record each cell's fastest variant in the tuned table: M = 1 keys "NxK" under the reference's section names,
+    small-batch keys "MxNxK" under "<fmt>_batch_shapes" ("batch_shapes" for BF16)."""
+    tuned = json.loads(f.read_text()) if f.exists() else {"platform": "mi355x", "shapes": {}}
+    for key, r in results.items():
+        if not r["ranked"]:
+            continue
+        if key.count("x") == 2:
+            sec = tuned.setdefault("batch_shapes" if fmt == "bf16" else f"{fmt}_batch_shapes", {})
+        else:
+            sec = tuned.setdefault(TKEY[fmt] if fmt != "int4zp" else "int4zp_shapes", {})
+        best = r["ranked"][0]
+        sec[key] = {"variant": best["variant"], "us": best["us"], "gbps": best["gbps"],
+                    "top5": [{"variant": x["variant"], "pct_of_best": 100 * best["us"] / x["us"]}
+                             for x in r["ranked"][:5]],
+                    "when": time.strftime("%Y-%m-%d %H:%M")}
+    f.parent.mkdir(parents=True, exist_ok=True)
+    f.write_text(json.dumps(tuned, indent=1))
 
 
 if __name__ == "__main__":

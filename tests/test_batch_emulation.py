@@ -14,6 +14,8 @@ The MFMA lane layout itself (A row l%16 / B column l%16 from k-group l/16; D row
 GPU tests check the kernel's output against the oracle, which fails for any other layout.
 """
 import itertools
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -212,6 +214,27 @@ TABLE = {
 }
 TABLE["int4zp"] = TABLE["int4"]
 WS = [(4, 1), (4, 2), (4, 4), (8, 1), (8, 2), (8, 4), (8, 8)]
+_TUNED = json.loads((Path(__file__).resolve().parents[1] / "paia-project_amd" / "tuned" / "mi355x.json").read_text())
+TUNED_BATCH = {f: _TUNED.get("batch_shapes" if f == "bf16" else f"{f}_batch_shapes", {})
+               for f in ("bf16", "fp8", "int4", "int4zp")}
+# row-streaming entries (P = 0): (R, U, W) x the M they serve; reported as (0, U, W, S=R, X=M)
+ROWS = [(1, 2, 8), (2, 2, 4), (1, 1, 8), (2, 1, 4), (1, 2, 16), (2, 1, 16)]
+ROWS_M = (2, 3, 4)
+
+
+def rows_lds(fmt, M, K):
+    """LDS of the row-streaming kernel (launch_gemv_rows): M staged copies of x, plus INT4 lane sums."""
+    row_bytes = {"bf16": 2 * K, "fp8": K}.get(fmt, K // 2)
+    nchunks = -(-row_bytes // 1024)
+    xq = {"bf16": 1, "fp8": 2}.get(fmt, 4)
+    return M * nchunks * (xq * 1024 + (256 if fmt.startswith("int4") else 0))
+
+
+def runs(fmt, M, N, K, v):
+    """Whether batch variant v runs at (M, N, K), or the entry point returns -2 first (LDS, or a row variant's M)."""
+    if v["P"] == 0:
+        return v["X"] == M and rows_lds(fmt, M, K) <= 65536
+    return plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"]) is not None
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4"])
@@ -234,12 +257,18 @@ def test_table_matches_library(gemv_lib):
     for fmt, k in KINDS.items():
         got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
         want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
+        want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M)}
         assert got == want, fmt
-        for M in (1, 2, 4, 8, 16):
+        for M in (1, 2, 3, 4, 8, 16):
             for N, K in [(4096, 4096), (28672, 4096), (4096, 14336), (4608, 3584), (3584, 18944), (128256, 4096)]:
                 v = L.batch_pick_variant(fmt, M, N, K)
                 assert 0 <= v < len(L.variants_batch[fmt])
                 d = L.variants_batch[fmt][v]
-                assert plan(fmt, M, N, K, d["P"], d["U"], d["W"], d["S"], d["X"]) is not None
+                assert runs(fmt, M, N, K, d), (fmt, M, N, K, d)
+                e = TUNED_BATCH.get(fmt, {}).get(f"{M}x{N}x{K}")
+                if e is not None:          # a measured entry wins
+                    assert all(d[k] == e["variant"][k] for k in "PUWSX"), (fmt, M, N, K, d, e)
+                else:                      # the rule: M = 2..4 stream the rows whenever their x copies fit
+                    assert (d["P"] == 0) == (2 <= M <= 4 and rows_lds(fmt, M, K) <= 65536), (fmt, M, N, K, d)
         assert L.batch_pick_variant(fmt, 17, 4096, 4096) == -1
         assert L.batch_pick_variant(fmt, 0, 4096, 4096) == -1

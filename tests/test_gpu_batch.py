@@ -13,7 +13,7 @@ import torch
 
 from gpu_util import bits16, dequant_oracle, make, note
 from paia_bench.inputs import to_device
-from test_batch_emulation import plan
+from test_batch_emulation import plan, runs
 
 pytestmark = pytest.mark.gpu
 
@@ -106,8 +106,9 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
             refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
             xd = x.to(cuda)
             for v in gemv_lib.variants_batch[fmt]:
-                if plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"]) is None:
-                    # S*M*U too large for the LDS chunk: the entry point refuses it (-2) before launching
+                if not runs(fmt, M, N, K, v):
+                    # S*M*U too large for the LDS chunk, or a row-streaming variant of another M: the entry point
+                    # refuses it (-2) before launching
                     with pytest.raises(RuntimeError, match="code -2"):
                         run_batch(gemv_lib, fmt, dev, xd, v["id"])
                     continue
@@ -116,6 +117,32 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
                 torch.cuda.synchronize()
                 worst = max(worst, check_rows(oracle, y, refs, f"{fmt} M={M} {N}x{K} v{v}"))
     print(f"batch {fmt}: worst relative error {worst:.2e}")
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
+def test_row_streaming_variants_awkward_shapes(oracle, gemv_lib, cuda, fmt):
+    """Every row-streaming variant (P = 0) at the M it serves (2, 3, 4) on the awkward shapes (N tails inside a row
+    group, K tails inside a chunk, single rows); shapes whose M copies of x exceed the LDS must return -2."""
+    worst = 0.0
+    rows_vs = [v for v in gemv_lib.variants_batch[fmt] if v["P"] == 0]
+    assert len(rows_vs) == 18
+    for N, K in AWK[fmt]:
+        ops, np_ops = make(fmt, N, K, bias=fmt != "int4")
+        dev = to_device(ops, cuda)
+        for M in (2, 3, 4):
+            x = x_rows(M, K, 3100 + M + N + K)
+            refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
+            xd = x.to(cuda)
+            for v in rows_vs:
+                if not runs(fmt, M, N, K, v):
+                    with pytest.raises(RuntimeError, match="code -2"):
+                        run_batch(gemv_lib, fmt, dev, xd, v["id"])
+                    continue
+                note(f"rows {fmt} M={M} N={N} K={K} variant={v}")
+                y = run_batch(gemv_lib, fmt, dev, xd, v["id"])
+                torch.cuda.synchronize()
+                worst = max(worst, check_rows(oracle, y, refs, f"{fmt} M={M} {N}x{K} v{v}"))
+    print(f"rows {fmt}: worst relative error {worst:.2e}")
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
