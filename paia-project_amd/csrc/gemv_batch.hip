@@ -109,8 +109,10 @@ bool fits(const BatchVariant& v, int M)
 //   * split-K S: at least two splits (every shape streamed faster with two waves per tile than with one), then the
 //     fewest (<= 8, >= 2 k-blocks each) that give >= 1152 work units (tiles x splits, 4.5 per CU): qkv (384 tiles)
 //     measured best at S = 4, o/down (256 tiles) at S = 8, gate_up (1792 tiles) at S = 2;
-//   * x in LDS (X=0) unless the splits x rows make staging cost more than it saves (M*S >= 32 with S >= 4: each block
-//     would stage half or more of its weight bytes again as x) or not even one chunk of U k-blocks fits;
+//   * x in LDS (X=0) unless the splits x rows make staging cost more than it saves (M*S >= 24 with S >= 4: each block
+//     would stage a third or more of its weight bytes again as x; measured at M = 3 on the tall-K down shapes, whose
+//     three x copies do not fit the row-streaming kernel: X=0 20.1 µs against 16.1 for X=1 at M = 4) or not even
+//     one chunk of U k-blocks fits;
 //   * one tile per wave; two when x comes with the weights and M >= 8, so the two tiles share each x load, provided
 //     the halved tile count still gives >= 1152 units within 8 splits (at 256 tiles it does not, and one tile per
 //     wave was faster there).
@@ -177,7 +179,7 @@ int pick(int kind, int M, int N, int K)
     const int U = kind >= 2 ? 4 : 2;
     int S = pick_splits(ntiles, KB, W);
     int P = 1, X = 0;
-    if ((M * S >= 32 && S >= 4) || batch_x_bytes(S, M, U) > kBatchLds) X = 1;
+    if ((M * S >= 24 && S >= 4) || batch_x_bytes(S, M, U) > kBatchLds) X = 1;
     if (X == 1 && M >= 8) {
         const int pairs = (ntiles + 1) / 2;
         const int S2 = pick_splits(pairs, KB, W);
