@@ -139,6 +139,9 @@ uint64_t rows_lds(int kind, int M, int K)
 int pick_rows(const Table& t, int kind, int M, int N, int K)
 {
     if (M < 2 || M > 4 || rows_lds(kind, M, K) > kMaxLds) return -1;
+    // INT4 at M = 4 on tall N: the four v_dot2 chains per decoded word saturate the VALU; the matrix cores were
+    // faster there (gate_up 28672x4096: 17.4 µs against 20.4; Qwen gate_up: 20.5 against 24.5)
+    if (kind >= 2 && M >= 4 && N >= 16384) return -1;
     int R = 1, U = 2, W = 8;
     const int v1 = paia_gemv_pick_variant(kind, N, K);
     int r = 0, u = 0, w = 0, s = 0, h = 1;
