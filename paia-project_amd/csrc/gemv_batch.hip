@@ -13,6 +13,8 @@
 // P = 0 marks the row-streaming kernel instead (gemv_rows_kernel: the M = 1 GEMV's weight stream and decode with one
 // accumulator per activation row, for M = 2..4): then U is its 1-KiB chunks per item, W its waves per block, S its
 // weight rows per wave (R) and X the one M it serves (other M: -2). These entries follow the matrix-core ones.
+// The last entry, P = U = W = S = 0 and X = 1, is the M = 1 GEMV itself (the M = 1 entry point's kernel and variant
+// choice) and serves M = 1 only.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -29,11 +31,8 @@ int launch_b(BatchParams p, hipStream_t st)
     return launch_batch<F, P, U, W, X>(p, st);
 }
 
-// the row-streaming kernel for exactly MB activation rows (weights streamed once: nt loads)
-template <int F, int R, int U, int W, int MB>
-int launch_rows_b(BatchParams b, hipStream_t st)
+GemvParams gemv_params(const BatchParams& b)
 {
-    if (b.M != MB) return -2;
     GemvParams p{};
     p.W = b.W;
     p.meta = b.meta;
@@ -46,11 +45,31 @@ int launch_rows_b(BatchParams b, hipStream_t st)
     p.row_bytes = b.row_bytes;
     p.meta_bytes = b.meta_bytes;
     p.zbytes = b.zbytes;
-    return launch_gemv_rows<F, R, U, W, 2, MB>(p, st);
+    return p;
+}
+
+// the row-streaming kernel for exactly MB activation rows (weights streamed once: nt loads)
+template <int F, int R, int U, int W, int MB>
+int launch_rows_b(BatchParams b, hipStream_t st)
+{
+    if (b.M != MB) return -2;
+    return launch_gemv_rows<F, R, U, W, 2, MB>(gemv_params(b), st);
+}
+
+// M = 1: the M = 1 GEMV with the library's M = 1 variant
+template <int F>
+int launch_m1_b(BatchParams b, hipStream_t st)
+{
+    if (b.M != 1) return -2;
+    const GemvParams p = gemv_params(b);
+    if (F == kBF16) return launch_gemv_bf16_picked(p, st);
+    if (F == kFP8) return launch_gemv_fp8_picked(p, st);
+    return launch_gemv_int4_picked(p, F == kI4ZP, st);
 }
 
 #define BV(F, P, U, W, S, X) {P, U, W, S, X, &launch_b<F, P, U, W, X>},
 #define RV(F, R, U, W, MB) {0, U, W, R, MB, &launch_rows_b<F, R, U, W, MB>},
+#define M1V(F) {0, 0, 0, 0, 1, &launch_m1_b<F>},
 #define RV_M(F, R, U, W) RV(F, R, U, W, 2) RV(F, R, U, W, 3) RV(F, R, U, W, 4)
 #define RV_ALL(F) RV_M(F, 1, 2, 8) RV_M(F, 2, 2, 4) RV_M(F, 1, 1, 8) RV_M(F, 2, 1, 4) RV_M(F, 1, 2, 16) \
                   RV_M(F, 2, 1, 16)
@@ -59,19 +78,21 @@ int launch_rows_b(BatchParams b, hipStream_t st)
 #define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1)
 // register budget: P * U * (16-byte loads per k-block) <= 16 buffers of 4 VGPRs (INT4 P=2 U=8 with x loaded
 // alongside spilled, so it is left out)
-const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2) RV_ALL(kBF16)};
+const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2) RV_ALL(kBF16)
+                                       M1V(kBF16)};
 const BatchVariant kFp8Batch[] = {BV_W(kFP8, 1, 2) BV_W(kFP8, 1, 4) BV_W(kFP8, 1, 8) BV_W(kFP8, 2, 2)
-                                      BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2) RV_ALL(kFP8)};
+                                      BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2) RV_ALL(kFP8) M1V(kFP8)};
 const BatchVariant kI4Batch[] = {BV_W(kI4, 1, 4) BV_W(kI4, 1, 8) BV_W(kI4, 2, 2) BV_W(kI4, 2, 4) BV_W(kI4, 4, 2)
-                                     BV_W(kI4, 4, 4) RV_ALL(kI4)};
+                                     BV_W(kI4, 4, 4) RV_ALL(kI4) M1V(kI4)};
 const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4ZP, 2, 2) BV_W(kI4ZP, 2, 4)
-                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4) RV_ALL(kI4ZP)};
+                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4) RV_ALL(kI4ZP) M1V(kI4ZP)};
 #undef BV
 #undef BV_S
 #undef BV_W
 #undef RV
 #undef RV_M
 #undef RV_ALL
+#undef M1V
 
 struct Table {
     const BatchVariant* v;
@@ -96,7 +117,7 @@ int find(const Table& t, int P, int U, int W, int S, int X)
 }
 
 // Whether variant v can run (M, K): X=0 needs a chunk of U k-blocks of x for all S splits in LDS; a row-streaming
-// variant serves its own M only (its LDS limit is checked at launch).
+// variant (and the M = 1 entry) serves its own M only (its LDS limit is checked at launch).
 bool fits(const BatchVariant& v, int M)
 {
     if (v.P == 0) return v.X == M;
@@ -104,8 +125,10 @@ bool fits(const BatchVariant& v, int M)
 }
 
 // Default choice: a measured entry for the shape and M when the tuned table has one; otherwise a rule fitted to MI355X
-// sweeps of the Llama/Qwen projection shapes (FP8 and INT4). M = 2..4 take the row-streaming kernel when its x copies
-// fit the LDS (pick_rows); otherwise the matrix-core kernel:
+// sweeps of the Llama/Qwen projection shapes (FP8 and INT4). M = 1 takes the M = 1 GEMV when its staged x fits the LDS
+// (it beat the matrix-core kernel on every BASELINE shape: FP8 gate_up 18.9 µs against 22.7, INT4 asymmetric 12.2
+// against 16.5). M = 2..4 take the row-streaming kernel when its x copies fit the LDS (pick_rows); otherwise the
+// matrix-core kernel:
 //   * split-K S: at least two splits (every shape streamed faster with two waves per tile than with one), then the
 //     fewest (<= 8, >= 2 k-blocks each) that give >= 1152 work units (tiles x splits, 4.5 per CU): qkv (384 tiles)
 //     measured best at S = 4, o/down (256 tiles) at S = 8, gate_up (1792 tiles) at S = 2;
@@ -174,6 +197,8 @@ int pick(int kind, int M, int N, int K)
             const int v = find(t, b.P, b.U, b.W, b.S, b.X);
             if (v >= 0 && fits(t.v[v], M)) return v;
         }
+    // the M = 1 GEMV's x (+ INT4 lane sums) and room for its split-K partials (W*R floats, <= 512 bytes)
+    if (M == 1 && rows_lds(kind, 1, K) + 512 <= kMaxLds) return find(t, 0, 0, 0, 0, 1);
     const int rv = pick_rows(t, kind, M, N, K);
     if (rv >= 0) return rv;
     const int W = 8;

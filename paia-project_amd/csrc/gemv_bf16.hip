@@ -52,6 +52,13 @@ int gemv_bf16_impl(const void* W, const void* x, const void* bias, void* y, int 
 
 }  // namespace
 
+namespace paia {
+int launch_gemv_bf16_picked(GemvParams p, hipStream_t st)
+{
+    return kBf16Variants[paia_gemv_pick_variant(0, p.N, p.K)].fn(p, st);
+}
+}  // namespace paia
+
 extern "C" {
 
 int paia_gemv_bf16_variant_count() { return kNumBf16; }

@@ -61,6 +61,13 @@ int gemv_fp8_impl(const void* Wq, const void* scale, const void* x, const void* 
 
 }  // namespace
 
+namespace paia {
+int launch_gemv_fp8_picked(GemvParams p, hipStream_t st)
+{
+    return kFp8Variants[paia_gemv_pick_variant(1, p.N, p.K)].fn(p, st);
+}
+}  // namespace paia
+
 extern "C" {
 
 int paia_gemv_fp8_variant_count() { return kNumFp8; }

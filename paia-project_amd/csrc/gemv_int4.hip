@@ -128,6 +128,14 @@ int default_bf16_variant()
 
 }  // namespace
 
+namespace paia {
+int launch_gemv_int4_picked(GemvParams p, bool zp, hipStream_t st)
+{
+    const int v = paia_gemv_pick_variant(zp ? 3 : 2, p.N, p.K);
+    return (zp ? kInt4ZpVariants : kInt4Variants)[v].fn(p, st);
+}
+}  // namespace paia
+
 extern "C" {
 
 int paia_gemv_int4_variant_count() { return kNumInt4; }

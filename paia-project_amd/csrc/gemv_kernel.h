@@ -649,9 +649,26 @@ int gemv_max_blocks_per_cu()
     return max_blocks_per_cu_of(gemv_kernel<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
 }
 
+// The busiest CU's row groups when `grid` blocks of W waves take `ng` groups in rounds of grid*W (block b, wave w
+// takes groups b*W + w + k*grid*W), block b running on CU b mod cus. That is CU 0: it holds the most blocks, and its
+// j-th block (b = j*cus) has the lowest index of all j-th blocks, so the last round reaches it first.
+inline int busiest_cu_groups(int ng, int grid, int W, int cus)
+{
+    const int full = ng / (grid * W), rem = ng - full * grid * W;
+    int load = 0;
+    for (int b = 0; b < grid; b += cus) {
+        const int tail = rem - b * W;
+        load += W * full + (tail <= 0 ? 0 : (tail < W ? tail : W));
+    }
+    return load;
+}
+
 // Persistent grid of a launch: blocks resident at once (occupancy, LDS, the waves-per-CU cap), then the groups per
 // wave (H=0) or per block (H=1) that cover N, at most 64/R per wave for H=0 so a wave's epilogue operands fit one
-// register (beyond that the grid grows past one resident wave of blocks).
+// register (beyond that the grid grows past one resident wave of blocks). H=0 with several blocks per CU and several
+// rounds: a whole number of blocks on every CU when that lowers the busiest CU's groups (the fewest blocks covering N
+// in q rounds leave some CUs a block more than others: BF16 gate_up 28672x4096 at 3.5 blocks per CU took 38.5 µs,
+// at 4 blocks per CU 35.2).
 template <int R, int W, bool KSPLIT>
 int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
 {
@@ -661,14 +678,22 @@ int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
     }
     if (per_cu > max_blocks_per_cu_for<W>()) per_cu = max_blocks_per_cu_for<W>();
-    const int gmax = (df.cus > 0 ? df.cus : 256) * per_cu;
+    const int cus = df.cus > 0 ? df.cus : 256;
+    const int gmax = cus * per_cu;
+    const int ng = p.ngroups;
     // units of work dealt round-robin: row groups to waves (H=0) or to blocks (H=1)
     const int per_block_units = KSPLIT ? 1 : W;
-    int grid = (p.ngroups + per_block_units - 1) / per_block_units;
+    int grid = (ng + per_block_units - 1) / per_block_units;
     if (grid > gmax) grid = gmax;
-    int q = (p.ngroups + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
+    int q = (ng + grid * per_block_units - 1) / (grid * per_block_units);   // units per wave / block
     if (!KSPLIT && q > kWave / R) q = kWave / R;
-    return (p.ngroups + q * per_block_units - 1) / (q * per_block_units);
+    const int fewest = (ng + q * per_block_units - 1) / (q * per_block_units);
+    if (KSPLIT || per_cu < 2 || q < 2) return fewest;
+    int b = ((ng + cus - 1) / cus + q * W - 1) / (q * W);   // blocks per CU for its share in q rounds
+    if (b > per_cu) b = per_cu;
+    const int even = cus * b;
+    if ((ng + even * W - 1) / (even * W) > q) return fewest;
+    return busiest_cu_groups(ng, even, W, cus) < busiest_cu_groups(ng, fewest, W, cus) ? even : fewest;
 }
 
 // Launch on `st`. Arguments were validated by the caller. Returns 0, -2 (LDS limit), or a hipError_t.
@@ -704,6 +729,13 @@ int launch_gemv_rows(GemvParams p, hipStream_t st)
 }
 
 using GemvLaunchFn = int (*)(GemvParams, hipStream_t);
+
+// The M = 1 kernel of a format with the library's variant for (N, K) (paia_gemv_pick_variant), p filled as that
+// format's M = 1 entry point fills it; 0, -2 (LDS limit) or a hipError_t. The small-batch entry points use these at
+// M = 1. zp: the asymmetric INT4 format.
+int launch_gemv_bf16_picked(GemvParams p, hipStream_t st);
+int launch_gemv_fp8_picked(GemvParams p, hipStream_t st);
+int launch_gemv_int4_picked(GemvParams p, bool zp, hipStream_t st);
 
 struct Variant {
     int R, U, W, S, H;

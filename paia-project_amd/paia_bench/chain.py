@@ -7,8 +7,8 @@ seed 1000 + N + K), checked against the CPU reference before timing; layers 1..3
 distributions on the device from a generator seeded 1000 + N + K + 7919. The whole chain (4.68 GB INT4, 8.04 GB FP8)
 streams from HBM on every replay; the 256 MiB Infinity Cache holds none of it across a replay.
 
-The launches are serialised exactly as in a decode step (one stream, each GEMV starts when the previous one has
-finished). The GEMV inputs x are fixed per launch: this chain measures the linear layers only; attention, norms and
+The launches are serialised exactly as in a decode step, in its order (layer by layer: qkv, o, gate_up, down; one
+stream, each GEMV starts when the previous one has finished). The GEMV inputs x are fixed per launch: this chain measures the linear layers only; attention, norms and
 activations that would sit between them are not part of the path.
 """
 from __future__ import annotations
@@ -24,9 +24,9 @@ from .timing import capture, replay_ms, stats
 def build_chain(lib, fmt: str, model: str = "llama31_8b", layers: int = 32, device="cuda", check: bool = True):
     """Returns (launch list, total algorithmic bytes, check results). fmt: 'int4zp' | 'fp8' (| 'bf16' | 'int4')."""
     dev = torch.device(device)
-    launches = []
     total = 0
     checks = {}
+    cases = []
     for nm, N, K in LAYER[model]:
         case = GemvCase(lib, fmt, N, K, name=f"{fmt}_{nm}_{N}x{K}")
         # copy 0 = the seeded CPU operands of layer 0 (checked), copies 1.. = per-layer device-seeded operands
@@ -34,9 +34,10 @@ def build_chain(lib, fmt: str, model: str = "llama31_8b", layers: int = 32, devi
         if check:
             rows = list(range(0, N, max(1, N // 64)))
             checks[case.name] = case.check(rows=rows)
-        for l in range(layers):
-            launches.append((case, l))
+        cases.append(case)
         total += layers * case.bytes()["total"]
+    # decode order: layer 0's qkv, o, gate_up, down, then layer 1's, ...
+    launches = [(case, l) for l in range(layers) for case in cases]
     N, K = LM_HEAD[model]
     head = GemvCase(lib, "bf16", N, K, name=f"bf16_lm_head_{N}x{K}")
     head.build(1, dev)

@@ -231,7 +231,10 @@ def rows_lds(fmt, M, K):
 
 
 def runs(fmt, M, N, K, v):
-    """Whether batch variant v runs at (M, N, K), or the entry point returns -2 first (LDS, or a row variant's M)."""
+    """Whether batch variant v runs at (M, N, K), or the entry point returns -2 first (LDS, or a row variant's M).
+    P = U = 0 is the M = 1 GEMV entry (its x, and any split-K partials, within the 64 KiB launch limit)."""
+    if v["P"] == 0 and v["U"] == 0:
+        return M == 1 and rows_lds(fmt, 1, K) + 512 <= 65536
     if v["P"] == 0:
         return v["X"] == M and rows_lds(fmt, M, K) <= 65536
     return plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"]) is not None
@@ -258,6 +261,8 @@ def test_table_matches_library(gemv_lib):
         got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
         want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
         want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M)}
+        want.add((0, 0, 0, 0, 1))                       # the M = 1 GEMV entry, last in each table
+        assert L.variants_batch[fmt][-1]["U"] == 0
         assert got == want, fmt
         for M in (1, 2, 3, 4, 8, 16):
             for N, K in [(4096, 4096), (28672, 4096), (4096, 14336), (4608, 3584), (3584, 18944), (128256, 4096)]:
@@ -268,7 +273,9 @@ def test_table_matches_library(gemv_lib):
                 e = TUNED_BATCH.get(fmt, {}).get(f"{M}x{N}x{K}")
                 if e is not None:          # a measured entry wins
                     assert all(d[k] == e["variant"][k] for k in "PUWSX"), (fmt, M, N, K, d, e)
-                else:                      # the rule: M = 2..4 stream the rows whenever their x copies fit
+                elif M == 1:               # the rule: M = 1 runs the M = 1 GEMV
+                    assert (d["P"], d["U"], d["X"]) == (0, 0, 1), (fmt, M, N, K, d)
+                else:                      # M = 2..4 stream the rows whenever their x copies fit
                     rows = 2 <= M <= 4 and rows_lds(fmt, M, K) <= 65536
                     rows = rows and not (fmt.startswith("int4") and M >= 4 and N >= 16384)
                     assert (d["P"] == 0) == rows, (fmt, M, N, K, d)

@@ -45,6 +45,15 @@ def lds_plan(fmt, nchunks, R, W, H):
     return base + part, part // gb
 
 
+def busiest_cu(ng, grid, W, cus):
+    """Row groups of the busiest CU, counted group by group: block b (on CU b mod cus), wave w takes groups
+    b*W + w + k*grid*W."""
+    load = [0] * cus
+    for g in range(ng):
+        load[(g % (grid * W)) // W % cus] += 1
+    return max(load)
+
+
 def launch(fmt, N, K, R, U, W, H, cus, per_cu):
     """Host sizing (launch_gemv): returns the params the kernel sees, or None for the -2 (LDS) case."""
     rb = row_bytes(fmt, K)
@@ -58,11 +67,17 @@ def launch(fmt, N, K, R, U, W, H, cus, per_cu):
         per_cu = 1                   # a 16-wave block runs alone on its CU
     gmax = cus * per_cu
     unit = 1 if H else W
-    grid = min(-(-p["ngroups"] // unit), gmax)
-    q = -(-p["ngroups"] // (grid * unit))
+    ng = p["ngroups"]
+    grid = min(-(-ng // unit), gmax)
+    q = -(-ng // (grid * unit))
     if not H:
         q = min(q, 64 // R)          # epilogue operands of all of a wave's groups in one register
-    grid = -(-p["ngroups"] // (q * unit))
+    grid = -(-ng // (q * unit))
+    if not H and per_cu >= 2 and q >= 2:
+        # a whole number of blocks per CU when that lowers the busiest CU's groups
+        b = min(-(-(-(-ng // cus)) // (q * W)), per_cu)
+        if -(-ng // (cus * b * W)) <= q and busiest_cu(ng, cus * b, W, cus) < busiest_cu(ng, grid, W, cus):
+            grid = cus * b
     p["grid"] = grid
     p["round"] = rnd
     return p
@@ -180,6 +195,23 @@ def test_lds_limit_matches_contract():
     assert launch("fp8", 8, 32768, 1, 1, 4, 0, 256, 1) is not None
     assert launch("int4", 8, 30720, 1, 1, 4, 0, 256, 1) is not None
     assert launch("int4", 8, 30848, 1, 1, 4, 0, 256, 1) is None
+
+
+def test_whole_blocks_per_cu_when_the_last_round_is_uneven():
+    """H=0 over several rounds and blocks per CU: the grid is a whole number of blocks per CU exactly when that lowers
+    the busiest CU's row groups (counted group by group), and never raises it or the rounds per wave."""
+    cases = {(14336, 8, 4): 1024, (18944, 8, 4): 1024, (10112, 8, 4): 768, (10368, 8, 4): 648, (9472, 4, 8): 1184,
+             (14336, 4, 8): 1792, (2048, 4, 8): 512}   # (groups, W, blocks per CU) -> grid on 256 CUs
+    for (ng, W, per_cu), want in cases.items():
+        p = launch("fp8", ng, 4096, 1, 1, W, 0, 256, per_cu)
+        assert p["grid"] == want, (ng, W, per_cu, p["grid"])
+    for ng, W, per_cu in itertools.product([300, 1000, 2049, 6000, 9999, 14336, 40000], [4, 8], [2, 4, 8]):
+        gmax = 256 * per_cu
+        q = min(-(-ng // (min(-(-ng // W), gmax) * W)), 64)
+        fewest = -(-ng // (q * W))
+        p = launch("fp8", ng, 4096, 1, 1, W, 0, 256, per_cu)
+        assert -(-ng // (p["grid"] * W)) <= q
+        assert busiest_cu(ng, p["grid"], W, 256) <= busiest_cu(ng, fewest, W, 256)
 
 
 def test_groups_per_wave_capped_for_the_epilogue_register():
