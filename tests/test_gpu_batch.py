@@ -236,6 +236,40 @@ def test_torch_ops_route_rows_to_batch_kernels(gemv_lib, cuda):
     assert torch.equal(y8.view(torch.int16), r8.view(torch.int16))
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
+def test_m1_runs_the_m1_gemv(gemv_lib, cuda, fmt):
+    """At M = 1 the batch pick is the M = 1 GEMV entry (the last of the table): bitwise equal to the M = 1 entry
+    point with its own pick, also into a y that is only 2-byte aligned (the batch contract; the BF16 M = 1 entry
+    point asks for 16)."""
+    L = gemv_lib
+    for N, K in [(4096, 4096), (37888, 3584), (1000, 3584), (33, {"bf16": 1032, "fp8": 1040}.get(fmt, 2176))]:
+        ops, _ = make(fmt, N, K, bias=fmt != "int4")
+        dev = to_device(ops, cuda)
+        x = x_rows(1, K, 5000 + N + K).to(cuda)
+        assert L.batch_pick_variant(fmt, 1, N, K) == len(L.variants_batch[fmt]) - 1
+        want = torch.full((N,), float("nan"), dtype=torch.bfloat16, device=cuda)
+        v = L.pick_variant(fmt, N, K)
+        b = dev.get("bias")
+        bp = b.data_ptr() if b is not None else None
+        note(f"batch M=1 route {fmt} {N}x{K} m1-variant={v}")
+        if fmt == "bf16":
+            L.bf16_bias(dev["W"].data_ptr(), x.data_ptr(), bp, want.data_ptr(), N, K, v)
+        elif fmt == "fp8":
+            L.fp8_bias(dev["Wq"].data_ptr(), dev["scale"].data_ptr(), x.data_ptr(), bp, want.data_ptr(), N, K, v)
+        elif fmt == "int4":
+            L.int4(dev["Wq"].data_ptr(), dev["scales"].data_ptr(), x.data_ptr(), want.data_ptr(), N, K, v)
+        else:
+            L.int4_zp(dev["Wq"].data_ptr(), dev["scales"].data_ptr(), dev["zeros"].data_ptr(), x.data_ptr(), bp,
+                      want.data_ptr(), N, K, v)
+        for off in (0, 1):                             # y at a 16-byte boundary, then 2 bytes past it
+            buf = torch.full((N + 8,), float("nan"), dtype=torch.bfloat16, device=cuda)
+            y = buf[off:off + N].view(1, N)
+            run_batch(L, fmt, dev, x, y=y)
+            torch.cuda.synchronize()
+            assert torch.equal(y[0].view(torch.int16), want.view(torch.int16)), (fmt, N, K, off)
+            assert torch.isnan(buf[off + N:]).all() and (off == 0 or torch.isnan(buf[:off]).all())
+
+
 def test_graph_capture_replays_match_eager(gemv_lib, cuda):
     """A captured batch call (split-K variant) replayed several times, with eager work and syncs between replays,
     matches the eager result every time."""
