@@ -11,8 +11,9 @@
 // K-chunk, 1 loaded with the weights). variant < 0 selects paia_gemv_batch_pick_variant's.
 //
 // P = 0 marks the row-streaming kernel instead (gemv_rows_kernel: the M = 1 GEMV's weight stream and decode with one
-// accumulator per activation row, for M = 2..4): then U is its 1-KiB chunks per item, W its waves per block, S its
-// weight rows per wave (R) and X the one M it serves (other M: -2). These entries follow the matrix-core ones.
+// accumulator per activation row, for M = 2..4, BF16 also 5..8): then U is its 1-KiB chunks per item, W its waves per
+// block, S its weight rows per wave (R) and X the one M it serves (other M: -2). These entries follow the matrix-core
+// ones.
 // The last entry, P = U = W = S = 0 and X = 1, is the M = 1 GEMV itself (the M = 1 entry point's kernel and variant
 // choice) and serves M = 1 only.
 #include <hip/hip_runtime.h>
@@ -73,13 +74,17 @@ int launch_m1_b(BatchParams b, hipStream_t st)
 #define RV_M(F, R, U, W) RV(F, R, U, W, 2) RV(F, R, U, W, 3) RV(F, R, U, W, 4)
 #define RV_ALL(F) RV_M(F, 1, 2, 8) RV_M(F, 2, 2, 4) RV_M(F, 1, 1, 8) RV_M(F, 2, 1, 4) RV_M(F, 1, 2, 16) \
                   RV_M(F, 2, 1, 16)
+// BF16 only (no decode: 4 v_dot2 per 16 weight bytes and activation row, so 8 rows stay within the VALU budget)
+#define RV_M8(F, R, U, W) RV(F, R, U, W, 5) RV(F, R, U, W, 6) RV(F, R, U, W, 7) RV(F, R, U, W, 8)
+#define RV_ALL8(F) RV_M8(F, 1, 2, 8) RV_M8(F, 2, 2, 4) RV_M8(F, 1, 1, 8) RV_M8(F, 2, 1, 4) RV_M8(F, 1, 2, 16) \
+                   RV_M8(F, 2, 1, 16)
 #define BV_S(F, P, U, X) BV(F, P, U, 4, 1, X) BV(F, P, U, 4, 2, X) BV(F, P, U, 4, 4, X) \
                          BV(F, P, U, 8, 1, X) BV(F, P, U, 8, 2, X) BV(F, P, U, 8, 4, X) BV(F, P, U, 8, 8, X)
 #define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1)
 // register budget: P * U * (16-byte loads per k-block) <= 16 buffers of 4 VGPRs (INT4 P=2 U=8 with x loaded
 // alongside spilled, so it is left out)
 const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2) RV_ALL(kBF16)
-                                       M1V(kBF16)};
+                                       RV_ALL8(kBF16) M1V(kBF16)};
 const BatchVariant kFp8Batch[] = {BV_W(kFP8, 1, 2) BV_W(kFP8, 1, 4) BV_W(kFP8, 1, 8) BV_W(kFP8, 2, 2)
                                       BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2) RV_ALL(kFP8) M1V(kFP8)};
 const BatchVariant kI4Batch[] = {BV_W(kI4, 1, 4) BV_W(kI4, 1, 8) BV_W(kI4, 2, 2) BV_W(kI4, 2, 4) BV_W(kI4, 4, 2)
@@ -92,6 +97,8 @@ const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4Z
 #undef RV
 #undef RV_M
 #undef RV_ALL
+#undef RV_M8
+#undef RV_ALL8
 #undef M1V
 
 struct Table {
@@ -127,7 +134,8 @@ bool fits(const BatchVariant& v, int M)
 // Default choice: a measured entry for the shape and M when the tuned table has one; otherwise a rule fitted to MI355X
 // sweeps of the Llama/Qwen projection shapes (FP8 and INT4). M = 1 takes the M = 1 GEMV when its staged x fits the LDS
 // (it beat the matrix-core kernel on every BASELINE shape: FP8 gate_up 18.9 µs against 22.7, INT4 asymmetric 12.2
-// against 16.5). M = 2..4 take the row-streaming kernel when its x copies fit the LDS (pick_rows); otherwise the
+// against 16.5). M = 2..4 (BF16 2..8) take the row-streaming kernel when its x copies fit the LDS (pick_rows; BF16 at
+// M = 5..8 measured 9-37% faster than the matrix cores on every BASELINE shape where it fits); otherwise the
 // matrix-core kernel:
 //   * split-K S: at least two splits (every shape streamed faster with two waves per tile than with one), then the
 //     fewest (<= 8, >= 2 k-blocks each) that give >= 1152 work units (tiles x splits, 4.5 per CU): qkv (384 tiles)
@@ -157,11 +165,11 @@ uint64_t rows_lds(int kind, int M, int K)
     return (uint64_t)M * nchunks * (xq * kChunkBytes + (kind >= 2 ? kWave * 4u : 0u));
 }
 
-// The row-streaming variant for M = 2..4: the M = 1 tuned choice's (R, U, W) when the table has that triple (the
-// weight stream is the M = 1 kernel's), else R=1 U=2 W=8. -1 when its x copies do not fit the LDS.
+// The row-streaming variant for M = 2..4 (BF16 2..8): the M = 1 tuned choice's (R, U, W) when the table has that
+// triple (the weight stream is the M = 1 kernel's), else R=1 U=2 W=8. -1 when its x copies do not fit the LDS.
 int pick_rows(const Table& t, int kind, int M, int N, int K)
 {
-    if (M < 2 || M > 4 || rows_lds(kind, M, K) > kMaxLds) return -1;
+    if (M < 2 || M > (kind == 0 ? 8 : 4) || rows_lds(kind, M, K) > kMaxLds) return -1;
     // INT4 at M = 4 on tall N: the four v_dot2 chains per decoded word saturate the VALU; the matrix cores were
     // faster there (gate_up 28672x4096: 17.4 µs against 20.4; Qwen gate_up: 20.5 against 24.5)
     if (kind >= 2 && M >= 4 && N >= 16384) return -1;

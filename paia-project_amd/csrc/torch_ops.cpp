@@ -9,8 +9,8 @@
 // Tensor-level surface (same semantics, same return-code errors surfaced as RuntimeError).
 //
 // x is [K], [1, K] or [M, K] with M <= 16 (y is [N], [1, N] or [M, N]). One activation row runs the M = 1 GEMV
-// kernels and `variant` indexes their table; M > 1 runs the small-batch matrix-core kernels (paia_gemv_batch_*) and
-// `variant` indexes the batch table of that format. -1 is the library's choice in both cases.
+// kernels and `variant` indexes their table; M > 1 runs the small-batch kernels (paia_gemv_batch_*: row-streaming or
+// matrix-core) and `variant` indexes the batch table of that format. -1 is the library's choice in both cases.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>

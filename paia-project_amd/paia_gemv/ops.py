@@ -5,8 +5,8 @@
     ops.gemv_int4_zp(Wq, s, z, x, bias=b, out=y)   # writes y, allocates nothing
 
 One activation row runs the M = 1 GEMV kernels (`variant` indexes GemvLib.variants / variants_fp8 / variants_int4);
-M = 2..16 rows run the small-batch matrix-core kernels (`variant` indexes GemvLib.variants_batch[fmt]); -1 is the
-library's choice.
+M = 2..16 rows run the small-batch kernels, row-streaming or matrix-core (`variant` indexes
+GemvLib.variants_batch[fmt]); -1 is the library's choice.
 
 The ops are registered by libpaia_gemv_torch.so (csrc/torch_ops.cpp); they run on torch's current stream and are
 HIP-graph capturable. There is no fallback: if the extension is missing, `load()` raises.

@@ -220,6 +220,7 @@ TUNED_BATCH = {f: _TUNED.get("batch_shapes" if f == "bf16" else f"{f}_batch_shap
 # row-streaming entries (P = 0): (R, U, W) x the M they serve; reported as (0, U, W, S=R, X=M)
 ROWS = [(1, 2, 8), (2, 2, 4), (1, 1, 8), (2, 1, 4), (1, 2, 16), (2, 1, 16)]
 ROWS_M = (2, 3, 4)
+ROWS_M_BF16 = (2, 3, 4, 5, 6, 7, 8)      # BF16 (no decode) streams up to 8 activation rows
 
 
 def rows_lds(fmt, M, K):
@@ -260,11 +261,11 @@ def test_table_matches_library(gemv_lib):
     for fmt, k in KINDS.items():
         got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
         want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
-        want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M)}
+        want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M_BF16 if fmt == "bf16" else ROWS_M)}
         want.add((0, 0, 0, 0, 1))                       # the M = 1 GEMV entry, last in each table
         assert L.variants_batch[fmt][-1]["U"] == 0
         assert got == want, fmt
-        for M in (1, 2, 3, 4, 8, 16):
+        for M in (1, 2, 3, 4, 5, 8, 16):
             for N, K in [(4096, 4096), (28672, 4096), (4096, 14336), (4608, 3584), (3584, 18944), (128256, 4096)]:
                 v = L.batch_pick_variant(fmt, M, N, K)
                 assert 0 <= v < len(L.variants_batch[fmt])
@@ -275,8 +276,8 @@ def test_table_matches_library(gemv_lib):
                     assert all(d[k] == e["variant"][k] for k in "PUWSX"), (fmt, M, N, K, d, e)
                 elif M == 1:               # the rule: M = 1 runs the M = 1 GEMV
                     assert (d["P"], d["U"], d["X"]) == (0, 0, 1), (fmt, M, N, K, d)
-                else:                      # M = 2..4 stream the rows whenever their x copies fit
-                    rows = 2 <= M <= 4 and rows_lds(fmt, M, K) <= 65536
+                else:                      # M = 2..4 (BF16 2..8) stream the rows whenever their x copies fit
+                    rows = 2 <= M <= (8 if fmt == "bf16" else 4) and rows_lds(fmt, M, K) <= 65536
                     rows = rows and not (fmt.startswith("int4") and M >= 4 and N >= 16384)
                     assert (d["P"] == 0) == rows, (fmt, M, N, K, d)
         assert L.batch_pick_variant(fmt, 17, 4096, 4096) == -1

@@ -121,16 +121,17 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
 def test_row_streaming_variants_awkward_shapes(oracle, gemv_lib, cuda, fmt):
-    """Every row-streaming variant (P = 0) at the M it serves (2, 3, 4), and the M = 1 GEMV entry at M = 1, on the
-    awkward shapes (N tails inside a row group, K tails inside a chunk, single rows); other M, and shapes whose M
-    copies of x exceed the LDS, must return -2."""
+    """Every row-streaming variant (P = 0) at the M it serves (2..4, BF16 2..8), and the M = 1 GEMV entry at M = 1,
+    on the awkward shapes (N tails inside a row group, K tails inside a chunk, single rows); other M, and shapes whose
+    M copies of x exceed the LDS, must return -2."""
     worst = 0.0
     rows_vs = [v for v in gemv_lib.variants_batch[fmt] if v["P"] == 0]
-    assert len(rows_vs) == 19
+    ms = (1, 2, 3, 4, 5, 6, 7, 8) if fmt == "bf16" else (1, 2, 3, 4)
+    assert len(rows_vs) == 6 * (len(ms) - 1) + 1
     for N, K in AWK[fmt]:
         ops, np_ops = make(fmt, N, K, bias=fmt != "int4")
         dev = to_device(ops, cuda)
-        for M in (1, 2, 3, 4):
+        for M in ms:
             x = x_rows(M, K, 3100 + M + N + K)
             refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
             xd = x.to(cuda)
