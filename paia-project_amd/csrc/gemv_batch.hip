@@ -11,7 +11,7 @@
 // K-chunk, 1 loaded with the weights). variant < 0 selects paia_gemv_batch_pick_variant's.
 //
 // P = 0 marks the row-streaming kernel instead (gemv_rows_kernel: the M = 1 GEMV's weight stream and decode with one
-// accumulator per activation row, for M = 2..4, BF16 and FP8 also 5..8): then U is its 1-KiB chunks per item, W its waves per
+// accumulator per activation row, for M = 2..6, BF16 and FP8 also 7, 8): then U is its 1-KiB chunks per item, W its waves per
 // block, S its weight rows per wave (R) and X the one M it serves (other M: -2). These entries follow the matrix-core
 // ones.
 // The last entry, P = U = W = S = 0 and X = 1, is the M = 1 GEMV itself (the M = 1 entry point's kernel and variant
@@ -74,10 +74,14 @@ int launch_m1_b(BatchParams b, hipStream_t st)
 #define RV_M(F, R, U, W) RV(F, R, U, W, 2) RV(F, R, U, W, 3) RV(F, R, U, W, 4)
 #define RV_ALL(F) RV_M(F, 1, 2, 8) RV_M(F, 2, 2, 4) RV_M(F, 1, 1, 8) RV_M(F, 2, 1, 4) RV_M(F, 1, 2, 16) \
                   RV_M(F, 2, 1, 16)
-// M = 5..8, BF16 and FP8: BF16 has no decode (4 v_dot2 per 16 weight bytes and activation row), so 8 rows stay within
-// the VALU budget and the default pick streams them; FP8 spends most of its VALU at M = 4 on the tall shapes, so only a
-// measured entry (the tuned table) picks these for it, where they beat the matrix cores
+// M = 5..8, BF16 and FP8 (INT4: 5, 6): BF16 has no decode (4 v_dot2 per 16 weight bytes and activation row), so 8 rows
+// stay within the VALU budget and the default pick streams them; FP8 and INT4 spend most of their VALU at M = 4 on the
+// tall shapes, so only a measured entry (the tuned table) picks these for them, where they beat the matrix cores
 #define RV_M8(F, R, U, W) RV(F, R, U, W, 5) RV(F, R, U, W, 6) RV(F, R, U, W, 7) RV(F, R, U, W, 8)
+// INT4 at M = 5, 6 (seven and eight rows of staged x and lane sums do not fit the 16-wave launch's 128 VGPRs)
+#define RV_M6(F, R, U, W) RV(F, R, U, W, 5) RV(F, R, U, W, 6)
+#define RV_ALL6(F) RV_M6(F, 1, 2, 8) RV_M6(F, 2, 2, 4) RV_M6(F, 1, 1, 8) RV_M6(F, 2, 1, 4) RV_M6(F, 1, 2, 16) \
+                   RV_M6(F, 2, 1, 16)
 #define RV_ALL8(F) RV_M8(F, 1, 2, 8) RV_M8(F, 2, 2, 4) RV_M8(F, 1, 1, 8) RV_M8(F, 2, 1, 4) RV_M8(F, 1, 2, 16) \
                    RV_M8(F, 2, 1, 16)
 #define BV_S(F, P, U, X) BV(F, P, U, 4, 1, X) BV(F, P, U, 4, 2, X) BV(F, P, U, 4, 4, X) \
@@ -90,9 +94,10 @@ const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF1
 const BatchVariant kFp8Batch[] = {BV_W(kFP8, 1, 2) BV_W(kFP8, 1, 4) BV_W(kFP8, 1, 8) BV_W(kFP8, 2, 2)
                                       BV_W(kFP8, 2, 4) BV_W(kFP8, 4, 2) RV_ALL(kFP8) RV_ALL8(kFP8) M1V(kFP8)};
 const BatchVariant kI4Batch[] = {BV_W(kI4, 1, 4) BV_W(kI4, 1, 8) BV_W(kI4, 2, 2) BV_W(kI4, 2, 4) BV_W(kI4, 4, 2)
-                                     BV_W(kI4, 4, 4) RV_ALL(kI4) M1V(kI4)};
+                                     BV_W(kI4, 4, 4) RV_ALL(kI4) RV_ALL6(kI4) M1V(kI4)};
 const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4ZP, 2, 2) BV_W(kI4ZP, 2, 4)
-                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4) RV_ALL(kI4ZP) M1V(kI4ZP)};
+                                       BV_W(kI4ZP, 4, 2) BV_W(kI4ZP, 4, 4) RV_ALL(kI4ZP) RV_ALL6(kI4ZP)
+                                       M1V(kI4ZP)};
 #undef BV
 #undef BV_S
 #undef BV_W
@@ -101,6 +106,8 @@ const BatchVariant kI4ZpBatch[] = {BV_W(kI4ZP, 1, 4) BV_W(kI4ZP, 1, 8) BV_W(kI4Z
 #undef RV_ALL
 #undef RV_M8
 #undef RV_ALL8
+#undef RV_M6
+#undef RV_ALL6
 #undef M1V
 
 struct Table {

@@ -175,14 +175,14 @@ struct ItemWalker {
     }
 };
 
-// The kernel body. MB activation rows (x [MB][K], y [MB][N]): MB = 1 is the M = 1 GEMV (gemv_kernel); MB = 2..4 (BF16, FP8:
+// The kernel body. MB activation rows (x [MB][K], y [MB][N]): MB = 1 is the M = 1 GEMV (gemv_kernel); MB = 2..6 (BF16, FP8:
 // 2..8) is the row-streaming small-batch kernel (gemv_rows_kernel): the same weight stream and decode, with MB
 // accumulators per row and MB staged copies of x, so each weight is loaded and decoded once for all activation rows.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB>
 __device__ __forceinline__ void gemv_body(const GemvParams& p)
 {
-    static_assert(MB >= 1 && MB <= 8 && (MB <= 4 || F == kBF16 || F == kFP8) && (MB == 1 || !KSPLIT),
-                  "activation rows: 1..4 (BF16, FP8 1..8), split-K only at M = 1");
+    static_assert(MB >= 1 && MB <= 8 && (MB <= 6 || F == kBF16 || F == kFP8) && (MB == 1 || !KSPLIT),
+                  "activation rows: 1..6 (BF16, FP8 1..8), split-K only at M = 1");
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -578,7 +578,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     gemv_body<F, R, U, W, AUX, KSPLIT, 1>(p);
 }
 
-// Small batch on the M = 1 design: MB = 2..4 (BF16 and FP8 2..8) activation rows, row-parallel (no split-K).
+// Small batch on the M = 1 design: MB = 2..6 (BF16 and FP8 2..8) activation rows, row-parallel (no split-K).
 template <int F, int R, int U, int W, int AUX, int MB>
 __global__ void __launch_bounds__(W * kWave) gemv_rows_kernel(GemvParams p)
 {

@@ -219,8 +219,8 @@ TUNED_BATCH = {f: _TUNED.get("batch_shapes" if f == "bf16" else f"{f}_batch_shap
                for f in ("bf16", "fp8", "int4", "int4zp")}
 # row-streaming entries (P = 0): (R, U, W) x the M they serve; reported as (0, U, W, S=R, X=M)
 ROWS = [(1, 2, 8), (2, 2, 4), (1, 1, 8), (2, 1, 4), (1, 2, 16), (2, 1, 16)]
-ROWS_M = (2, 3, 4)
 ROWS_M8 = (2, 3, 4, 5, 6, 7, 8)      # BF16 and FP8 have row-streaming variants up to 8 activation rows
+ROWS_M6 = (2, 3, 4, 5, 6)            # INT4 up to 6
 
 
 def rows_lds(fmt, M, K):
@@ -261,7 +261,7 @@ def test_table_matches_library(gemv_lib):
     for fmt, k in KINDS.items():
         got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
         want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
-        want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M8 if fmt in ("bf16", "fp8") else ROWS_M)}
+        want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M8 if fmt in ("bf16", "fp8") else ROWS_M6)}
         want.add((0, 0, 0, 0, 1))                       # the M = 1 GEMV entry, last in each table
         assert L.variants_batch[fmt][-1]["U"] == 0
         assert got == want, fmt

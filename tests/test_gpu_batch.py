@@ -121,12 +121,12 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
 def test_row_streaming_variants_awkward_shapes(oracle, gemv_lib, cuda, fmt):
-    """Every row-streaming variant (P = 0) at the M it serves (2..4, BF16 and FP8 2..8), and the M = 1 GEMV entry at M = 1,
+    """Every row-streaming variant (P = 0) at the M it serves (2..6, BF16 and FP8 2..8), and the M = 1 GEMV entry at M = 1,
     on the awkward shapes (N tails inside a row group, K tails inside a chunk, single rows); other M, and shapes whose
     M copies of x exceed the LDS, must return -2."""
     worst = 0.0
     rows_vs = [v for v in gemv_lib.variants_batch[fmt] if v["P"] == 0]
-    ms = (1, 2, 3, 4, 5, 6, 7, 8) if fmt in ("bf16", "fp8") else (1, 2, 3, 4)
+    ms = (1, 2, 3, 4, 5, 6, 7, 8) if fmt in ("bf16", "fp8") else (1, 2, 3, 4, 5, 6)
     assert len(rows_vs) == 6 * (len(ms) - 1) + 1
     for N, K in AWK[fmt]:
         ops, np_ops = make(fmt, N, K, bias=fmt != "int4")
