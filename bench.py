@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the paia_gemv hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH] [--no-cpu] [--no-chain]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH] [--no-cpu] [--no-chain] [--no-b0]
 
 Workload (the metric's configuration): FP8 W8A16 M=1 GEMVs at the Llama-3.1-8B per-layer shapes
 qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336, OCP e4m3fn weights with a per-row fp32 scale, bf16
@@ -17,6 +17,9 @@ Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmi
   roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time (hipEvents on the launch
                 stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels of known size
+  b0            the streaming-read probe in the same run (the reference's measured-bandwidth denominator "B0"): the
+                best rate of a 2 GiB read, and the read floor for each GEMV's byte count under the same cold-cache
+                rotation; per_gemv then also carries % of B0 and the GEMV time over that floor (skipped with --no-b0)
   chain         BASELINE configs[4]: 32 layers x 4 GEMVs + bf16 lm_head as one hipGraph, INT4 (asymmetric g128) and
                 FP8: us per token-step and aggregate GB/s (skipped with --no-chain)
   cpu_baseline  the CPU path (oracle dequantisation + torch fp32 matmul) on the host cores, on a bounded sample
@@ -43,6 +46,33 @@ PEAK_GBPS = 8000.0
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def measure_b0(dev, cases, per: dict) -> dict:
+    """B0 (the reference's measured streaming-read bandwidth, src/tests/gemv_bf16_check.cu:228-252) in this run: the
+    best rate of a 2 GiB nontemporal read over a few launch shapes, then, for each GEMV case, the read floor for its
+    byte count (reads of that size rotating over the 2 GiB buffer, back to back in one graph). Adds pct_of_b0 and
+    over_read_floor (GEMV µs / floor µs) to each per_gemv entry."""
+    import torch
+    from paia_bench.probe import b0_large, b0_sized, load_probe
+
+    P = load_probe()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    buf = torch.empty(2 * 2 ** 30, dtype=torch.uint8, device=dev)
+    buf.random_(0, 255)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    gbps, cfg = b0_large(P, buf, sink, cus, configs=((4, 1), (8, 1), (8, 4), (16, 1), (16, 4)), log=lambda m: None)
+    sized = {}
+    for c in cases:
+        r = b0_sized(P, buf, sink, cus, c.bytes()["total"])
+        sized[c.name] = {"bytes": r["bytes"], "us": round(r["us"], 3), "gbps": round(r["gbps"], 1)}
+        e = per[c.name]
+        e["pct_of_b0"] = round(100 * e["gbps"] / gbps, 1)
+        e["over_read_floor"] = round(e["us"] / r["us"], 3)
+    del buf
+    torch.cuda.empty_cache()
+    return {"gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "bytes": 2 * 2 ** 30,
+            "blocks_per_cu": cfg[0], "unroll": cfg[1], "read_floor": sized}
 
 
 def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
@@ -126,6 +156,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--report", type=str, default=None, help="also write a detailed JSON report here")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-b0", action="store_true", help="skip the streaming-read probe (B0) leg")
     ap.add_argument("--no-chain", action="store_true", help="skip the decode-chain (configs[4]) measurement")
     a = ap.parse_args(argv)
     if a.gpus != 1:
@@ -226,6 +257,12 @@ def main(argv=None):
             "algorithmic_bytes": dom.bytes()["total"],
             "traffic_detail": traffic}
 
+    b0 = None
+    if not a.no_b0:
+        log("streaming-read probe (B0) ...")
+        b0 = measure_b0(dev, cases, per)
+        log(f"  b0 {b0['gbps']:.0f} GB/s ({b0['pct_of_8TBps']:.1f}% of 8 TB/s)")
+
     chain = None
     if not a.no_chain:
         from paia_bench.chain import run_chain
@@ -252,7 +289,7 @@ def main(argv=None):
                       "layer_copies": L, "rotation_bytes": L * layer_bytes, "step_bytes": step_bytes,
                       "us_per_layer_step": round(ms_per_step * 1e3, 3),
                       "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1), "timed_graph_primed": True},
-           "per_gemv": per, "roofline": roof, "chain": chain, "cpu_baseline": cpu}
+           "per_gemv": per, "roofline": roof, "b0": b0, "chain": chain, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
     if a.report:
         Path(a.report).parent.mkdir(parents=True, exist_ok=True)

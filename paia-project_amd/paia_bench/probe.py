@@ -31,6 +31,55 @@ def load_probe():
     return lib
 
 
+def b0_large(P, buf, sink, cus, configs=((2, 1), (2, 4), (2, 8), (4, 1), (4, 4), (4, 8), (8, 1), (8, 4), (8, 8),
+                                         (16, 1), (16, 4), (16, 8), (32, 1), (32, 4), (32, 8)), log=print):
+    """B0: the best streaming-read rate (GB/s) over (blocks per CU, unroll) configs, reading all of `buf` three times
+    per graph replay (median of 5 replays). Returns (GB/s, (blocks per CU, unroll))."""
+    from paia_gemv.loader import current_raw_stream
+
+    from .timing import capture, replay_ms, stats
+    total = buf.numel()
+
+    def read(grid, unroll):
+        rc = P.paia_probe_read(buf.data_ptr(), total, sink.data_ptr(), grid, unroll, current_raw_stream())
+        if rc:
+            raise RuntimeError(f"probe rc {rc}")
+    best = (0.0, None)
+    for mult, unroll in configs:
+        g = capture(lambda: [read(cus * mult, unroll) for _ in range(3)], warm=1)
+        ms = stats(replay_ms(g, 5))["median"] / 3
+        del g
+        gbps = total / (ms * 1e-3) / 1e9
+        log(f"[b0] grid {cus}x{mult} unroll {unroll}: {gbps:.0f} GB/s")
+        if gbps > best[0]:
+            best = (gbps, (mult, unroll))
+    return best
+
+
+def b0_sized(P, buf, sink, cus, S: int, mults=(4, 8, 16)) -> dict:
+    """The read floor for S bytes: reads of S bytes from distinct slices of `buf`, back to back in one graph (the
+    GEMV timings' cold-cache rotation); the best µs per read over the grid sizes."""
+    from paia_gemv.loader import current_raw_stream
+
+    from .timing import capture, replay_ms, stats
+    S16 = (S + 255) // 256 * 256
+    n = max(2, buf.numel() // S16)
+    R = min(2000, max(50, int(5e-3 / (S / 6e12))))
+
+    def read(ptr, grid):
+        rc = P.paia_probe_read(ptr, S, sink.data_ptr(), grid, 4, current_raw_stream())
+        if rc:
+            raise RuntimeError(f"probe rc {rc}")
+    best = None
+    for mult in mults:
+        g = capture(lambda: [read(buf.data_ptr() + (j % n) * S16, cus * mult) for j in range(R)], warm=1)
+        us = stats(replay_ms(g, 5))["median"] * 1e3 / R
+        del g
+        if best is None or us < best[0]:
+            best = (us, mult)
+    return {"bytes": S, "us": best[0], "gbps": S / (best[0] * 1e-6) / 1e9, "grid_per_cu": best[1]}
+
+
 def main(argv=None):
     import torch
 
@@ -51,22 +100,8 @@ def main(argv=None):
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     res = {"cus": cus}
 
-    def read(ptr, nbytes, grid, unroll):
-        rc = P.paia_probe_read(ptr, nbytes, sink.data_ptr(), grid, unroll, current_raw_stream())
-        if rc:
-            raise RuntimeError(f"probe rc {rc}")
-
     # B0 large
-    best = (0, None)
-    for mult in (2, 4, 8, 16, 32):
-        for unroll in (1, 4, 8):
-            g = capture(lambda: [read(buf.data_ptr(), total, cus * mult, unroll) for _ in range(3)], warm=1)
-            ms = stats(replay_ms(g, 5))["median"] / 3
-            gbps = total / (ms * 1e-3) / 1e9
-            print(f"[b0] grid {cus}x{mult} unroll {unroll}: {gbps:.0f} GB/s", flush=True)
-            if gbps > best[0]:
-                best = (gbps, (mult, unroll))
-            del g
+    best = b0_large(P, buf, sink, cus, log=lambda m: print(m, flush=True))
     res["b0_gbps"] = best[0]
     res["b0_cfg"] = {"grid_per_cu": best[1][0], "unroll": best[1][1]}
     print(f"[b0] best {best[0]:.0f} GB/s ({100 * best[0] / HBM_PEAK_GBPS:.1f}% of 8 TB/s) at {best[1]}", flush=True)
@@ -78,19 +113,9 @@ def main(argv=None):
             sizes[f"{fmt}_{N}x{K}"] = gemv_bytes(fmt, N, K)["total"]
     res["sized"] = {}
     for key, S in sorted(sizes.items(), key=lambda kv: kv[1]):
-        S16 = (S + 255) // 256 * 256
-        n = max(2, total // S16)
-        R = min(2000, max(50, int(5e-3 / (S / 6e12))))
-        bestg = None
-        for mult in (4, 8, 16):
-            g = capture(lambda: [read(buf.data_ptr() + (j % n) * S16, S, cus * mult, 4) for j in range(R)], warm=1)
-            us = stats(replay_ms(g, 5))["median"] * 1e3 / R
-            del g
-            if bestg is None or us < bestg[0]:
-                bestg = (us, mult)
-        res["sized"][key] = {"bytes": S, "us": bestg[0], "gbps": S / (bestg[0] * 1e-6) / 1e9, "grid_per_cu": bestg[1]}
-        print(f"[b0 sized] {key:22s} {S / 2**20:8.2f} MiB  {bestg[0]:7.2f} us  {S / (bestg[0] * 1e-6) / 1e9:6.0f} GB/s",
-              flush=True)
+        r = b0_sized(P, buf, sink, cus, S)
+        res["sized"][key] = r
+        print(f"[b0 sized] {key:22s} {S / 2**20:8.2f} MiB  {r['us']:7.2f} us  {r['gbps']:6.0f} GB/s", flush=True)
 
     # launch floor
     for grid in (1, 256, 2048):
