@@ -100,7 +100,8 @@ PAIA_API int paia_quantize_int4_zp_g128(const void* W, void* packed, void* scale
  * format, 3 INT4 asymmetric (an index of the paia_gemv_int4 table). Always returns a valid index of that table. */
 PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
 
-/* ---- small batch: M = 1..16 activation rows on the matrix cores. No reference symbol: the reference's kernels are
+/* ---- small batch: M = 1..16 activation rows (matrix-core kernel, row-streaming kernel on the M = 1 design, and the
+ * M = 1 GEMV itself at M = 1; the library picks per shape and M). No reference symbol: the reference's kernels are
  * M = 1 only and M = 1..16 is its open item (src/README.md:118, swept by paia-bench/configs/shapes.yaml:63-64).
  * x bf16 [M][K] row-major (16-byte aligned), y bf16 [M][N] row-major (2-byte aligned); the weight operands, their
  * alignment and the K rules are those of the M = 1 entry point of the same format. bias bf16 [N] or NULL.

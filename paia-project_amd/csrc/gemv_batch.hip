@@ -1,4 +1,5 @@
-// Small-batch (M = 1..16) GEMV C ABI on the matrix cores: variant tables, argument checks, launch.
+// Small-batch (M = 1..16) GEMV C ABI: variant tables (matrix-core, row-streaming and M = 1 entries), argument checks,
+// pick, launch.
 //
 // No reference symbol: the reference's kernels are M = 1 only, and M = 1..16 is its open item (src/README.md:118)
 // that its harness sweeps for library GEMMs (paia-bench/configs/shapes.yaml:63-64). The entry points take the same
