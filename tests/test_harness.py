@@ -103,3 +103,26 @@ def test_tuned_table_drives_pick_variant(gemv_lib):
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_sweep_merge_writes_the_faster_cell(tmp_path):
+    """`paia_bench.sweep --merge A B --write-tuned T`: per cell the faster of the files' best variants, M = 1 cells
+    under the format's section, "MxNxK" cells under its batch section, and existing entries of other cells kept."""
+    from paia_bench import sweep
+
+    def res(us_m1, us_b, v_b):
+        return {"fmt": "fp8", "results": {
+            "4096x4096": {"ranked": [{"variant": {"R": 2, "U": 2, "W": 4, "S": 0, "H": 0}, "us": us_m1, "gbps": 1.0}]},
+            "5x4096x4096": {"ranked": [{"variant": v_b, "us": us_b, "gbps": 1.0}]},
+            "8x1x1": {"ranked": []}}}
+    rows = {"P": 0, "U": 2, "W": 8, "S": 1, "X": 5}
+    mfma = {"P": 1, "U": 2, "W": 8, "S": 8, "X": 1}
+    a, b, t = tmp_path / "a.json", tmp_path / "b.json", tmp_path / "t.json"
+    a.write_text(json.dumps(res(5.0, 6.5, rows)))
+    b.write_text(json.dumps(res(4.0, 7.7, mfma)))
+    t.write_text(json.dumps({"platform": "mi355x", "fp8_shapes": {"1x2": {"variant": {}}}}))
+    assert sweep.main(["--fmt", "fp8", "--merge", str(a), str(b), "--write-tuned", str(t)]) == 0
+    out = json.loads(t.read_text())
+    assert out["fp8_shapes"]["4096x4096"]["us"] == 4.0 and "1x2" in out["fp8_shapes"]
+    assert out["fp8_batch_shapes"]["5x4096x4096"]["variant"] == rows
+    assert "8x1x1" not in out["fp8_batch_shapes"]
