@@ -112,7 +112,8 @@ PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
  * per item, W waves per block, S weight rows per wave, and X the one M (2-6; BF16 and FP8 2-8) it serves. The last variant of
  * each table (P = U = W = S = 0, X = 1) is the M = 1 GEMV itself with paia_gemv_pick_variant's choice (M = 1 only;
  * the batch alignment rules hold for it, y included). Returns 0, -1 bad variant, -2 bad shape/alignment (or, X = 0,
- * S*M*U too large for the LDS chunk; or, P = 0, another M or M copies of the staged x beyond 64 KiB of LDS), > 0
+ * S*M*U too large for the LDS chunk; or, P = 0, another M or M copies of the staged x beyond the device's per-block
+ * LDS, 160 KiB on MI355X), > 0
  * hipError_t. */
 PAIA_API int paia_gemv_batch_variant_count(int kind);
 PAIA_API int paia_gemv_batch_variant_info(int kind, int v, int* P, int* U, int* W, int* S, int* X);

@@ -179,7 +179,7 @@ uint64_t rows_lds(int kind, int M, int K)
 // triple (the weight stream is the M = 1 kernel's), else R=1 U=2 W=8. -1 when its x copies do not fit the LDS.
 int pick_rows(const Table& t, int kind, int M, int N, int K)
 {
-    if (M < 2 || M > (kind == 0 ? 8 : 4) || rows_lds(kind, M, K) > kMaxLds) return -1;
+    if (M < 2 || M > (kind == 0 ? 8 : 4) || rows_lds(kind, M, K) > rows_max_lds()) return -1;
     // INT4 at M = 4 on tall N: the four v_dot2 chains per decoded word saturate the VALU; the matrix cores were
     // faster there (gate_up 28672x4096: 17.4 µs against 20.4; Qwen gate_up: 20.5 against 24.5)
     if (kind >= 2 && M >= 4 && N >= 16384) return -1;
@@ -213,7 +213,10 @@ int pick(int kind, int M, int N, int K)
     for (const BatchPick& b : kBatchTuned)
         if (b.kind == kind && b.M == M && b.N == N && b.K == K) {
             const int v = find(t, b.P, b.U, b.W, b.S, b.X);
-            if (v >= 0 && fits(t.v[v], M)) return v;
+            // a row-streaming entry also needs its x copies to fit this device's LDS (the entries were measured with
+            // MI355X's 160 KiB per block)
+            const bool lds_ok = b.P != 0 || b.U == 0 || rows_lds(kind, M, K) <= rows_max_lds();
+            if (v >= 0 && fits(t.v[v], M) && lds_ok) return v;
         }
     // the M = 1 GEMV's x (+ INT4 lane sums) and room for its split-K partials (W*R floats, <= 512 bytes)
     if (M == 1 && rows_lds(kind, 1, K) + 512 <= kMaxLds) return find(t, 0, 0, 0, 0, 1);

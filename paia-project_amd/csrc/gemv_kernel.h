@@ -593,6 +593,7 @@ __global__ void __launch_bounds__(W * kWave) gemv_rows_kernel(GemvParams p)
 struct DeviceFacts {
     int cus = 0;
     int lds_per_cu = 0;
+    int lds_per_block = 0;
 };
 DeviceFacts device_facts();
 
@@ -711,8 +712,16 @@ int launch_gemv(GemvParams p, hipStream_t st)
     return (int)hipGetLastError();
 }
 
+// LDS the row-streaming launch may request: the device's per-block limit (160 KiB on MI355X), at least kMaxLds. A block
+// that large runs alone on its CU, which suits the 16-wave variants.
+inline uint32_t rows_max_lds()
+{
+    const int l = device_facts().lds_per_block;
+    return l > (int)kMaxLds ? (uint32_t)l : kMaxLds;
+}
+
 // The row-streaming small-batch launch: MB activation rows (x [MB][K], y [MB][N]); LDS holds MB copies of the
-// staged x (and INT4 lane sums). Returns -2 when they exceed kMaxLds.
+// staged x (and INT4 lane sums). Returns -2 when they exceed rows_max_lds().
 template <int F, int R, int U, int W, int AUX, int MB>
 int launch_gemv_rows(GemvParams p, hipStream_t st)
 {
@@ -721,7 +730,17 @@ int launch_gemv_rows(GemvParams p, hipStream_t st)
     p.ngroups = (p.N + R - 1) / R;
     p.round = 1;
     const uint64_t lds = (uint64_t)MB * (lds_x_bytes<F>(p.nchunks) + lds_s32_bytes<F>(p.nchunks));
-    if (lds > kMaxLds) return -2;
+    if (lds > rows_max_lds()) return -2;
+    if (lds > kMaxLds) {   // beyond the default dynamic-LDS limit: raise it once for this kernel
+        static std::atomic<int> raised{0};
+        if (!raised.load(std::memory_order_relaxed)) {
+            const hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&gemv_rows_kernel<F, R, U, W, AUX, MB>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)rows_max_lds());
+            if (e != hipSuccess) return (int)e;
+            raised.store(1, std::memory_order_relaxed);
+        }
+    }
     static std::atomic<int> cached{0};
     const int per_cu = max_blocks_per_cu_of(gemv_rows_kernel<F, R, U, W, AUX, MB>, W * kWave, cached);
     const int grid = gemv_grid<R, W, false>(p, (uint32_t)lds, per_cu);

@@ -13,7 +13,7 @@ import torch
 
 from gpu_util import bits16, dequant_oracle, make, note
 from paia_bench.inputs import to_device
-from test_batch_emulation import plan, runs
+from test_batch_emulation import plan, rows_lds_limit, runs
 
 pytestmark = pytest.mark.gpu
 
@@ -106,7 +106,7 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
             refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
             xd = x.to(cuda)
             for v in gemv_lib.variants_batch[fmt]:
-                if not runs(fmt, M, N, K, v):
+                if not runs(fmt, M, N, K, v, rows_lds_limit()):
                     # S*M*U too large for the LDS chunk, or a row-streaming variant of another M: the entry point
                     # refuses it (-2) before launching
                     with pytest.raises(RuntimeError, match="code -2"):
@@ -136,7 +136,7 @@ def test_row_streaming_variants_awkward_shapes(oracle, gemv_lib, cuda, fmt):
             refs = oracle_rows(oracle, fmt, np_ops, xbits(x))
             xd = x.to(cuda)
             for v in rows_vs:
-                if not runs(fmt, M, N, K, v):
+                if not runs(fmt, M, N, K, v, rows_lds_limit()):
                     with pytest.raises(RuntimeError, match="code -2"):
                         run_batch(gemv_lib, fmt, dev, xd, v["id"])
                     continue
