@@ -4,7 +4,7 @@ Counterpart of src/tools/dev_sweep_bf16.py:30-100 for gfx950: same idea (time ea
 graph timing and rotation, keep the best and the top five), same tuned-table schema keyed "NxK" under "shapes" /
 "fp8_shapes" / "int4_shapes" (paia-bench/bench/ops/ours_bf16.py:32-38, ours_quant.py:29-36).
 
-    python -m paia_bench.sweep --fmt fp8 --shapes baseline --out gpurun_out/sweep_fp8.json
+    python -m paia_bench.sweep --fmt fp8 --shapes baseline --out OUT/sweep_fp8.json
     python -m paia_bench.sweep --fmt int4zp --shapes baseline --write-tuned paia-project_amd/tuned/mi355x.json
     python -m paia_bench.sweep --fmt fp8 --shapes baseline --batch 1,2,4,8,16     # small-batch kernels (P,U,W,S)
     python -m paia_bench.sweep --fmt fp8 --shapes frozen --candidates tuned --write-tuned paia-project_amd/tuned/mi355x.json
