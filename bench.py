@@ -2,29 +2,38 @@
 """Benchmark of the paia_gemv hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--report PATH] [--no-cpu] [--no-chain] [--no-b0]
+                    [--no-per-gemv]
 
 Workload (the metric's configuration): FP8 W8A16 M=1 GEMVs at the Llama-3.1-8B per-layer shapes
 qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336, OCP e4m3fn weights with a per-row fp32 scale, bf16
 activations and outputs. One step = the four GEMVs of one decoder layer; steps rotate over L distinct layer copies
 whose total (>= 4 x 256 MiB) defeats the Infinity Cache, so every weight byte comes from HBM. The timed region is one
 hipGraph replay of K steps (that graph launched once, untimed, beforehand), bracketed by device synchronisation,
-with all inputs resident in HBM. Each GEMV uses the library's per-shape variant (paia_gemv_pick_variant, the frozen MI355X
-sweep in paia-project_amd/tuned/mi355x.json).
+with all inputs resident in HBM. Each GEMV uses the library's per-shape variant (paia_gemv_pick_variant, the frozen
+MI355X sweep in paia-project_amd/tuned/mi355x.json).
 
 Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmic GB/s of the step, plus
-  per_gemv      us/GEMV, GB/s and % of 8 TB/s for each shape (graph of R back-to-back launches rotating over
-                >= 4 x 256 MiB of copies of that shape alone)
-  roofline      the dominant kernel (gate_up): algorithmic bytes / its average launch time (hipEvents on the launch
-                stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the committed rocprofv3
-                FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels of known size
+  per_gemv      us/GEMV, GB/s and % of 8 TB/s for every GEMV of the BASELINE configs, each shape on its own graph
+                of R back-to-back launches rotating over >= 4 x 256 MiB of copies of that shape alone: configs[0]
+                BF16 o_proj, configs[1] the four FP8 Llama shapes, configs[2] the four INT4 (asymmetric g128) Llama
+                shapes, configs[3] the Qwen2.5-7B shapes in all three formats (qkv with its bias) and the bf16
+                lm_head, configs[4]'s bf16 Llama lm_head; every case's copy 0 gated against the CPU reference first
+  roofline      the dominant kernel of the workload (FP8 gate_up): algorithmic bytes / its average launch time
+                (hipEvents on the launch stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the
+                committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels
+                of known size. roofline_by_dtype: the same for each format's dominant Llama GEMV
   b0            the streaming-read probe in the same run (the reference's measured-bandwidth denominator "B0"): the
-                best rate of a 2 GiB read, and the read floor for each GEMV's byte count under the same cold-cache
+                best rate of a 2 GiB (less 1 MiB) read, and the read floor for each GEMV's byte count under the same cold-cache
                 rotation; per_gemv then also carries % of B0 and the GEMV time over that floor (skipped with --no-b0)
   chain         BASELINE configs[4]: 32 layers x 4 GEMVs + bf16 lm_head as one hipGraph, INT4 (asymmetric g128) and
-                FP8: us per token-step and aggregate GB/s (skipped with --no-chain)
-  cpu_baseline  the CPU path (oracle dequantisation + torch fp32 matmul) on the host cores, on a bounded sample
+                FP8: us per token-step and aggregate GB/s; layer 0 gated before capture, layers 0, 1, 31 and the head
+                after the replays (skipped with --no-chain)
+  cpu_baseline  the reference's CPU path: the paia_gemv.quant torch dequantisation
+                (src/paia_gemv/quant.py semantics) and a torch fp32 matmul (paia-bench/bench/ops/ours_quant.py:69-71)
+                on the host cores, per configuration, timed (i) dequant + matmul and (ii) matmul on pre-dequantised
+                weights, median of 5 after 2 warm-ups; value = the FP8 layer step's GB/s under (i)
 Copy 0 of every operand set is checked against the CPU fp32 reference (torch dequantisation + matmul, the reference
-harness's gate) before anything is timed. The CPU oracle is used only by the cpu_baseline leg, as the CPU path timed.
+harness's gate) before anything is timed. The CPU oracle is not used here.
 """
 from __future__ import annotations
 
@@ -32,6 +41,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -42,6 +52,24 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "µs/GEMV + achieved HBM GB/s (% of 8 TB/s), Llama-3.1-8B shapes, batch 1"
 PEAK_GBPS = 8000.0
+B0_BYTES = 2 * 2 ** 30 - 2 ** 20   # the B0 read (the GEMV-path probe takes < 2 GiB per launch)
+
+# Every M = 1 GEMV of the BASELINE configs: (config, format, model, projection, N, K, bias)
+LLAMA = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+QWEN = [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
+PER_GEMV = ([("configs[1]", "fp8", "llama", nm, N, K, False) for nm, N, K in LLAMA]
+            + [("configs[0]", "bf16", "llama", "o", 4096, 4096, False)]
+            + [("configs[2]", "int4zp", "llama", nm, N, K, False) for nm, N, K in LLAMA]
+            + [("configs[3]", f, "qwen", nm, N, K, nm == "qkv") for f in ("bf16", "fp8", "int4zp") for nm, N, K in QWEN]
+            + [("configs[3]", "bf16", "qwen", "lm_head", 152064, 3584, False),
+               ("configs[4]", "bf16", "llama", "lm_head", 128256, 4096, False)])
+# each format's dominant Llama GEMV (roofline_by_dtype): configs[0]'s only shape for BF16, gate_up otherwise
+DOMINANT = {"bf16": "bf16_llama_o_4096x4096", "fp8": "fp8_llama_gate_up_28672x4096",
+            "int4zp": "int4zp_llama_gate_up_28672x4096"}
+
+
+def case_name(fmt, model, nm, N, K, bias):
+    return f"{fmt}_{model}_{nm}{'_bias' if bias else ''}_{N}x{K}"
 
 
 def log(msg):
@@ -50,79 +78,114 @@ def log(msg):
 
 def measure_b0(dev, cases, per: dict) -> dict:
     """B0 (the reference's measured streaming-read bandwidth, src/tests/gemv_bf16_check.cu:228-252) in this run: the
-    best rate of a 2 GiB nontemporal read over a few launch shapes, then, for each GEMV case, the read floor for its
-    byte count (reads of that size rotating over the 2 GiB buffer, back to back in one graph). Adds pct_of_b0 and
+    best rate of a 2 GiB (less 1 MiB) read over the probe's launch shapes, then, for each GEMV case, the read floor for its byte
+    count (reads of that size rotating over the 2 GiB buffer, back to back in one graph). Adds pct_of_b0 and
     over_read_floor (GEMV µs / floor µs) to each per_gemv entry."""
     import torch
     from paia_bench.probe import b0_large, b0_sized, load_probe
 
     P = load_probe()
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    buf = torch.empty(2 * 2 ** 30, dtype=torch.uint8, device=dev)
+    buf = torch.empty(B0_BYTES, dtype=torch.uint8, device=dev)
     buf.random_(0, 255)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    gbps, cfg = b0_large(P, buf, sink, cus, configs=((4, 1), (8, 1), (8, 4), (16, 1), (16, 4)), log=lambda m: None)
+    gbps, cfg = b0_large(P, buf, sink, cus, log=lambda m: None)
     sized = {}
-    for c in cases:
-        r = b0_sized(P, buf, sink, cus, c.bytes()["total"])
-        sized[c.name] = {"bytes": r["bytes"], "us": round(r["us"], 3), "gbps": round(r["gbps"], 1)}
-        e = per[c.name]
+    for name, nbytes in cases:
+        r = b0_sized(P, buf, sink, cus, nbytes)
+        sized[name] = {"bytes": r["bytes"], "us": round(r["us"], 3), "gbps": round(r["gbps"], 1), "cfg": r["cfg"]}
+        e = per[name]
         e["pct_of_b0"] = round(100 * e["gbps"] / gbps, 1)
         e["over_read_floor"] = round(e["us"] / r["us"], 3)
     del buf
     torch.cuda.empty_cache()
-    return {"gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "bytes": 2 * 2 ** 30,
-            "blocks_per_cu": cfg[0], "unroll": cfg[1], "read_floor": sized}
+    return {"gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "bytes": B0_BYTES,
+            "cfg": cfg, "read_floor": sized}
 
 
-def cpu_baseline(oracle, cases, budget_s: float = 12.0) -> dict:
-    """The reference's CPU path (dequantise, then an fp32 matmul): the oracle's C dequantiser
-    (one thread) and torch's CPU fp32 matmul on the host cores, over the layer's four shapes (seeded copy-0 operands)
-    until ~budget_s."""
+def cpu_model() -> str:
     import platform
-
-    import torch
-    from paia_bench.inputs import as_numpy
-
-    threads = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64"))))
-    torch.set_num_threads(threads)
-    t_deq = t_mm = 0.0
-    nbytes = 0
-    steps = 0
-    t_start = time.perf_counter()
-    while True:
-        for c in cases:
-            a = as_numpy(c.ops0)
-            t0 = time.perf_counter()
-            Wd = oracle.dequant_fp8(a["Wq"], a["scale"])
-            t1 = time.perf_counter()
-            x = torch.from_numpy(oracle.bf16_bits_to_f32(a["x"]).copy())
-            y = torch.from_numpy(Wd) @ x
-            y = y.to(torch.bfloat16)
-            t2 = time.perf_counter()
-            t_deq += t1 - t0
-            t_mm += t2 - t1
-            nbytes += c.bytes()["total"]
-            del Wd, y
-        steps += 1
-        if time.perf_counter() - t_start > budget_s or steps >= 20:
-            break
-    total = t_deq + t_mm
-    model = ""
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
-        model = platform.processor()
-    return {"value": round(nbytes / total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} layer step(s) x 4 FP8 GEMVs (Llama-3.1-8B qkv/o/gate_up/down, seeded copy 0): "
-                      f"oracle C dequant (1 thread) + torch fp32 matmul ({threads} threads); "
-                      f"us per layer step {total / steps * 1e6:.0f} (dequant {t_deq / steps * 1e6:.0f}, "
-                      f"matmul {t_mm / steps * 1e6:.0f}); cpu {model}",
-            "us_per_layer_step": round(total / steps * 1e6, 1),
-            "matmul_only_gbps": round(nbytes / t_mm / 1e9, 3) if t_mm > 0 else None}
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(lib, budget_s: float = 30.0) -> dict:
+    """The reference's CPU path: for each configuration the seeded operands of the GPU run
+    (paia_bench.inputs.make_operands, CPU generator seeded 1000 + N + K), dequantised with paia_gemv.quant's torch
+    definitions (the formulas of src/paia_gemv/quant.py:16-17,34-38; (q - z) * s for the asymmetric INT4 format) and
+    multiplied x.float() @ Wdeq.t() in fp32 (paia-bench/bench/ops/ours_quant.py:69-71, cublas_bf16.py:36), + bias,
+    rounded to bf16. Timed per configuration as (i) dequant + matmul and (ii) matmul on pre-dequantised weights,
+    median of 5 runs after 2 warm-ups (time.perf_counter_ns), on all the host cores this process may use.
+    `value`: the FP8 Llama layer step (configs[1], the metric's workload) under (i), in algorithmic GB/s."""
+    import torch
+    from paia_bench.inputs import make_operands
+    from paia_gemv import quant
+    from paia_gemv.shapes import gemv_bytes
+
+    threads = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))          # the box's CPU share for this job
+    torch.set_num_threads(threads)
+    configs = ([("configs[1]", "fp8", nm, N, K) for nm, N, K in LLAMA] +
+               [("configs[2]", "int4zp", nm, N, K) for nm, N, K in LLAMA] +
+               [("configs[0]", "bf16", "o", 4096, 4096)])
+    rows = []
+    t_start = time.perf_counter()
+    for cfg, fmt, nm, N, K in configs:
+        o = make_operands(fmt, N, K)
+        x = o["x"].float()[None, :]
+
+        def deq():
+            if fmt == "fp8":
+                return quant.dequant_fp8(o["Wq"], o["scale"])
+            if fmt == "int4zp":
+                return quant.dequant_int4_zp(o["Wq"], o["scales"], o["zeros"])
+            return o["W"].float()
+
+        def full():
+            return (x @ deq().t()).to(torch.bfloat16)
+
+        Wd = deq()
+
+        def mm():
+            return (x @ Wd.t()).to(torch.bfloat16)
+
+        def med(fn, reps=5, warm=2):
+            for _ in range(warm):
+                fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter_ns()
+                fn()
+                ts.append(time.perf_counter_ns() - t0)
+            return statistics.median(ts) / 1e3
+        us_full, us_mm = med(full), med(mm)
+        nbytes = gemv_bytes(fmt, N, K)["total"]
+        rows.append({"config": cfg, "gemv": f"{fmt}_llama_{nm}_{N}x{K}", "bytes": nbytes,
+                     "us_dequant_matmul": round(us_full, 1), "us_matmul": round(us_mm, 1),
+                     "gbps_dequant_matmul": round(nbytes / us_full / 1e3, 3),
+                     "gbps_matmul": round(nbytes / us_mm / 1e3, 3)})
+        del Wd, o
+        if time.perf_counter() - t_start > budget_s:
+            break
+    step = [r for r in rows if r["config"] == "configs[1]"]
+    step_us = sum(r["us_dequant_matmul"] for r in step)
+    step_bytes = sum(r["bytes"] for r in step)
+    return {"value": round(step_bytes / step_us / 1e3, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"one pass per run over each BASELINE configuration ({len(rows)} GEMVs: FP8 and INT4-asym "
+                      f"Llama-3.1-8B qkv/o/gate_up/down, BF16 o), seeded copy-0 operands; paia_gemv.quant torch "
+                      f"dequant + torch fp32 matmul (x.float() @ Wdeq.t()), {threads} threads, median of 5 after 2 "
+                      f"warm-ups; value = FP8 layer step (configs[1]) {step_us:.0f} us under dequant+matmul; "
+                      f"cpu {cpu_model()}",
+            "us_per_fp8_layer_step": round(step_us, 1),
+            "us_per_fp8_layer_step_matmul_only": round(sum(r["us_matmul"] for r in step), 1),
+            "cpu": cpu_model(), "per_config": rows}
 
 
 def load_traffic(case_name: str):
@@ -135,18 +198,57 @@ def load_traffic(case_name: str):
         d = json.loads(f.read_text())
         e = d.get("cases", {}).get(case_name)
         return None if e is None else {"bytes": round(e["traffic_bytes"]), "kernel": e.get("kernel"),
-                                       "fetch_bytes": round(e["fetch_bytes"]), "write_bytes": round(e["write_bytes"])}
+                                       "fetch_bytes": round(e["fetch_bytes"]), "write_bytes": round(e["write_bytes"]),
+                                       "over_algorithmic": e.get("traffic_over_algorithmic")}
     except (OSError, ValueError, KeyError):
         return None
 
 
-def kernel_name(lib, case) -> str:
+def kernel_name(lib, fmt, variant) -> str:
     """The template instance of gemv_kernel a case launches (as rocprofv3 names it)."""
-    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(case.fmt, lib.variants_int4)
-    v = fam[case.variant]
-    F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[case.fmt]
-    aux = (2 if v["S"] else 0) if case.fmt == "bf16" else 2
+    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
+    v = fam[variant]
+    F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[fmt]
+    aux = (2 if v["S"] else 0) if fmt == "bf16" else 2
     return f"paia::gemv_kernel<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
+
+
+def roofline_entry(lib, name, e):
+    traffic = load_traffic(name)
+    return {"bound": "hbm", "achieved": e["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": round(e["gbps"] / PEAK_GBPS, 4), "traffic": traffic["bytes"] if traffic else None,
+            "kernel": e["kernel"], "case": name, "avg_launch_us": e["us"], "algorithmic_bytes": e["bytes"],
+            "traffic_detail": traffic}
+
+
+def measure_per_gemv(lib, dev) -> dict:
+    """Every GEMV of PER_GEMV on its own rotation (>= 4 x 256 MiB of copies of that shape), copy 0 gated first."""
+    import torch
+    from paia_bench.cases import GemvCase
+    from paia_bench.chain import sample_rows
+    from paia_bench.timing import plan_rotation, time_per_call_us
+
+    per = {}
+    for cfg, fmt, model, nm, N, K, bias in PER_GEMV:
+        name = case_name(fmt, model, nm, N, K, bias)
+        c = GemvCase(lib, fmt, N, K, bias=bias, name=name)
+        n_rot = plan_rotation(c.footprint())["n_copies"]
+        c.build(n_rot, dev, host_copy0=False)
+        c.call(0)
+        chk = c.check_copy(0, sample_rows(N, 256))
+        if not chk["ok"]:
+            raise RuntimeError(f"{name} failed the correctness gate: {chk}")
+        t = time_per_call_us(c.call, n_rot)
+        c.free()
+        torch.cuda.empty_cache()
+        gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
+        fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
+        per[name] = {"config": cfg, "us": round(t["us"], 3), "gbps": round(gbps, 1),
+                     "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "variant": fam[c.variant],
+                     "kernel": kernel_name(lib, fmt, c.variant), "bytes": c.bytes()["total"], "R": t["R"],
+                     "copies": n_rot, "rel_err": round(chk["rel_err"], 5)}
+        log(f"  {name}: {t['us']:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s)")
+    return per
 
 
 def main(argv=None):
@@ -158,6 +260,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-b0", action="store_true", help="skip the streaming-read probe (B0) leg")
     ap.add_argument("--no-chain", action="store_true", help="skip the decode-chain (configs[4]) measurement")
+    ap.add_argument("--no-per-gemv", action="store_true", help="skip the per-GEMV figures (and b0, roofline)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}). The M=1 GEMV shards along N "
@@ -167,9 +270,8 @@ def main(argv=None):
 
     import torch
     from paia_bench.cases import GemvCase
-    from paia_bench.timing import LLC_BYTES, capture, plan_rotation, time_per_call_us
+    from paia_bench.timing import LLC_BYTES, capture
     from paia_gemv import load_lib
-    from paia_gemv.shapes import LAYER
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (MI355X)", file=sys.stderr)
@@ -179,8 +281,7 @@ def main(argv=None):
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} CUs {props.multi_processor_count} lib {lib.path}")
 
-    shapes = LAYER["llama31_8b"]
-    cases = [GemvCase(lib, "fp8", N, K, name=f"fp8_{nm}_{N}x{K}") for nm, N, K in shapes]
+    cases = [GemvCase(lib, "fp8", N, K, name=case_name("fp8", "llama", nm, N, K, False)) for nm, N, K in LLAMA]
     layer_bytes = sum(c.footprint() for c in cases)
     L = max(2, math.ceil(4 * LLC_BYTES / layer_bytes))
     for c in cases:
@@ -228,40 +329,20 @@ def main(argv=None):
     log(f"timed {a.steps} steps: {gpu_ms:.3f} ms (wall {wall_ms:.3f} ms), {ms_per_step * 1e3:.2f} us/step, "
         f"{value:.0f} GB/s")
     del g_warm, g_timed
-
-    # per-GEMV figures: each shape on its own, rotating over enough copies of that shape alone (>= 4 x 256 MiB), so
-    # the small shapes cannot run out of the Infinity Cache (the layer's L copies of one o_proj are only 84 MB)
     for c in cases:
         c.free()
     torch.cuda.empty_cache()
-    per = {}
-    for c in cases:
-        n_rot = plan_rotation(c.footprint())["n_copies"]
-        c.build(n_rot, dev)
-        t = time_per_call_us(c.call, n_rot)
-        c.free()
-        torch.cuda.empty_cache()
-        gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
-        per[c.name] = {"us": round(t["us"], 3), "gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1),
-                       "variant": lib.variants_fp8[c.variant], "kernel": kernel_name(lib, c),
-                       "bytes": c.bytes()["total"], "R": t["R"], "copies": n_rot}
-        log(f"  {c.name}: {t['us']:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s)")
 
-    dom = max(cases, key=lambda c: c.bytes()["total"])
-    dom_us = per[dom.name]["us"]
-    achieved = dom.bytes()["total"] / (dom_us * 1e-6) / 1e9
-    traffic = load_traffic(dom.name)
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic["bytes"] if traffic else None,
-            "kernel": kernel_name(lib, dom), "case": dom.name, "avg_launch_us": dom_us,
-            "algorithmic_bytes": dom.bytes()["total"],
-            "traffic_detail": traffic}
-
-    b0 = None
-    if not a.no_b0:
-        log("streaming-read probe (B0) ...")
-        b0 = measure_b0(dev, cases, per)
-        log(f"  b0 {b0['gbps']:.0f} GB/s ({b0['pct_of_8TBps']:.1f}% of 8 TB/s)")
+    per, roof, by_dtype, b0 = {}, None, {}, None
+    if not a.no_per_gemv:
+        per = measure_per_gemv(lib, dev)
+        dom = DOMINANT["fp8"]
+        roof = roofline_entry(lib, dom, per[dom])
+        by_dtype = {f: roofline_entry(lib, n, per[n]) for f, n in DOMINANT.items()}
+        if not a.no_b0:
+            log("streaming-read probe (B0) ...")
+            b0 = measure_b0(dev, [(n, e["bytes"]) for n, e in per.items()], per)
+            log(f"  b0 {b0['gbps']:.0f} GB/s ({b0['pct_of_8TBps']:.1f}% of 8 TB/s)")
 
     chain = None
     if not a.no_chain:
@@ -271,14 +352,9 @@ def main(argv=None):
 
     cpu = None
     if not a.no_cpu:
-        from oracle import oracle
         log("cpu baseline ...")
-        from paia_bench.inputs import make_operands
-        cpu_cases = [GemvCase(lib, "fp8", N, K, name=f"fp8_{nm}_{N}x{K}") for nm, N, K in shapes]
-        for c in cpu_cases:
-            c.ops0 = make_operands("fp8", c.N, c.K)
-        cpu = cpu_baseline(oracle, cpu_cases)
-        log(f"  cpu {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(lib)
+        log(f"  cpu {cpu['value']:.2f} GB/s on {cpu['cores']} threads (FP8 layer step {cpu['us_per_fp8_layer_step']:.0f} us)")
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
@@ -289,7 +365,8 @@ def main(argv=None):
                       "layer_copies": L, "rotation_bytes": L * layer_bytes, "step_bytes": step_bytes,
                       "us_per_layer_step": round(ms_per_step * 1e3, 3),
                       "pct_of_8TBps": round(100 * value / PEAK_GBPS, 1), "timed_graph_primed": True},
-           "per_gemv": per, "roofline": roof, "b0": b0, "chain": chain, "cpu_baseline": cpu}
+           "roofline": roof, "roofline_by_dtype": by_dtype, "per_gemv": per, "b0": b0, "chain": chain,
+           "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
     if a.report:
         Path(a.report).parent.mkdir(parents=True, exist_ok=True)

@@ -11,9 +11,11 @@
  *   x, y and bias are bf16 bit patterns; N, K are ints with size_t offsets inside.
  *   y[n] = bf16_round_to_nearest_even( sum_k deq(W[n,k]) * x[k] (+ bias[n]) ), fp32 accumulation.
  *
- * gfx950 limit that the reference does not have: x is staged in LDS, so K is bounded by 64 KiB of LDS per block:
- *   BF16 and FP8 K <= 32768, INT4 K <= 30720 (all Llama-3.1-8B / Qwen2.5-7B shapes fit); larger K returns -2.
- *   Split-K variants (H=1) also keep one round of partial sums in that LDS: BF16 K <= 32256, FP8 K <= 31744.
+ * K: every K of the alignment rules runs, as in the reference. x is staged in 64 KiB of LDS per block up to BF16 and
+ *   FP8 K <= 32768, INT4 K <= 30720 (split-K variants (H=1) also keep one round of partial sums there: BF16
+ *   K <= 32256, FP8 K <= 31744); beyond that the call runs an x-from-global kernel (x read with each item's weights,
+ *   split-K over 8 waves) whatever the variant, slower but with the same contract. All Llama-3.1-8B / Qwen2.5-7B
+ *   shapes stage x.
  */
 #ifndef PAIA_GEMV_H
 #define PAIA_GEMV_H

@@ -4,6 +4,11 @@
 //   keeps the loads alive -- the MI355X counterpart of the reference's dev read probe "B0"
 //   (src/tests/gemv_bf16_check.cu:131-139,228-252). Timing it on the same byte counts as a GEMV gives the achievable
 //   bandwidth (and the fixed cost) that kernel is measured against.
+// paia_probe_stream: the same read through the GEMV's own load path: raw buffer loads (16 bytes per lane, nt) of
+//   1-KiB chunks, U chunks per item, two items in flight per wave, items dealt round-robin to the waves of a
+//   persistent grid of blocks_per_cu blocks of W waves on every CU (the walk of the fused GEMV at R = 1, H = 0,
+//   without x, the decode or the store). The benchmark takes the best of both probes, over their launch shapes, as
+//   the read floor.
 // paia_probe_copy: a plain 16-byte-per-lane copy of known size, the calibration kernel for the rocprofv3 byte counters
 //   (FETCH_SIZE should read its size once, WRITE_SIZE its size once).
 // paia_probe_empty: an empty kernel, for the per-launch floor of back-to-back launches in a graph.
@@ -32,6 +37,76 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads from being removed
+}
+
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+
+// Reads nbytes (< 2^31) once. Item i = bytes [i*U KiB, (i+1)*U KiB): wave w of block b takes items b*W + w + k*grid*W.
+// Two item buffers, each refilled right after it is consumed; items past the end load at an out-of-range offset (no
+// traffic). The loop is left by `return` when a wave's items run out, as the GEMV's loop is. The loads come from
+// read-only memory, so the compiler may move them to their first use (then only one item is in flight): an empty
+// asm barrier after each issue keeps them in place, and the exit folds both buffers (zeros there) into the sink.
+template <int U, int W>
+__global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __restrict__ buf, uint32_t nbytes,
+                                                              uint32_t* sink)
+{
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(buf, nbytes);
+    const uint32_t lane16 = (threadIdx.x & 63u) * 16u;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    constexpr uint32_t item_bytes = U * 1024u;
+    const uint32_t nitems = (nbytes + item_bytes - 1) / item_bytes;
+    uint32_t item = blockIdx.x * W + wave;
+    const uint32_t stride = gridDim.x * W;
+    uint32_t acc = 0;
+    u32x4 b[2][U];
+    bool valid[2];
+    auto issue = [&](int d) {
+        valid[d] = item < nitems;
+        const uint32_t off = valid[d] ? item * item_bytes + lane16 : kOOB;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            b[d][u] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + u * 1024u, 0u, 2));
+        item += stride;
+        asm volatile("" ::: "memory");   // compiler barrier: the loads stay where they are issued (no sinking)
+    };
+    auto consume = [&](int d) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= b[d][u].x ^ b[d][u].y ^ b[d][u].z ^ b[d][u].w;
+    };
+    issue(0);
+    issue(1);
+    // one exit test per trip (two would merge into one exit block whose false edge reaches the loop header, and the
+    // wait counts would then assume the newest loads are the ones consumed first); the trip's second item may lie
+    // past the end: its loads return zeros without traffic
+    for (;;) {
+        if (!valid[0]) {
+            consume(0);
+            consume(1);
+            if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads alive
+            return;
+        }
+        consume(0);
+        __builtin_amdgcn_sched_barrier(0);   // keep each refill after the consume of its buffer
+        issue(0);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int U, int W>
+int launch_stream(const void* buf, uint32_t nbytes, uint32_t* sink, int grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((stream_probe_kernel<U, W>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink);
+    return (int)hipGetLastError();
 }
 
 __global__ void __launch_bounds__(256) copy_probe_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
@@ -63,6 +138,24 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     default: return -1;
     }
     return (int)hipGetLastError();
+}
+
+// U in {1, 2, 4, 8}, W in {4, 8, 16}; grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
+__attribute__((visibility("default"))) int paia_probe_stream(const void* buf, size_t nbytes, void* sink, int U, int W,
+                                                             int grid, void* stream)
+{
+    if (!buf || !sink || (reinterpret_cast<uintptr_t>(buf) & 15) || grid <= 0 || nbytes == 0 || nbytes >= (1ull << 31))
+        return -2;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* s = static_cast<uint32_t*>(sink);
+    const uint32_t n = (uint32_t)nbytes;
+#define PROBE_CASE(UU, WW) \
+    if (U == UU && W == WW) return launch_stream<UU, WW>(buf, n, s, grid, st);
+#define PROBE_W(UU) PROBE_CASE(UU, 4) PROBE_CASE(UU, 8) PROBE_CASE(UU, 16)
+    PROBE_W(1) PROBE_W(2) PROBE_W(4) PROBE_W(8)
+#undef PROBE_W
+#undef PROBE_CASE
+    return -1;
 }
 
 __attribute__((visibility("default"))) int paia_probe_copy(const void* src, void* dst, size_t nbytes, int grid,

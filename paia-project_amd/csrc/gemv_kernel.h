@@ -90,6 +90,22 @@ __device__ __forceinline__ void x_load(const uint16_t* x, int K, XRegs<XE>& xr)
     for (int e = 0; e < XE; ++e) xr.v[e] = ld16<0>(xrs, ((uint32_t)threadIdx.x + (uint32_t)(e * NT)) * 16u, 0u);
 }
 
+// INT4: the sum of one x vector's 8 values (fixed order), and the vector re-paired (x0,x2),(x4,x6),(x1,x3),(x5,x7)
+// to match the nibble order of i4_word_dot.
+__device__ __forceinline__ float i4_pair_sum_x(u32x4& v)
+{
+    const float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
+                      (bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16))) +
+                     ((bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16)) +
+                      (bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16)));
+    const u32x4 a = v;
+    v.x = (a.x & 0xFFFFu) | (a.y << 16);
+    v.y = (a.z & 0xFFFFu) | (a.w << 16);
+    v.z = (a.x >> 16) | (a.y & 0xFFFF0000u);
+    v.w = (a.z >> 16) | (a.w & 0xFFFF0000u);
+    return s8;
+}
+
 template <int F>
 __device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
 {
@@ -97,19 +113,10 @@ __device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
     const int c = q / (XQ * kWave), r = q - c * (XQ * kWave);
     const int l = r / XQ, j = r - l * XQ;
     if constexpr (F == kI4 || F == kI4ZP) {
-        // segment sum of this vector's 8 values (fixed order), then over the quad = the lane's 32 columns
-        float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
-                    (bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16))) +
-                   ((bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16)) +
-                    (bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16)));
-        s8 = quad_sum(s8);   // the 4 vectors of a lane-segment are 4 consecutive q in one quad of threads
+        // the 4 vectors of a lane-segment are 4 consecutive q in one quad of threads: the quad sum is the lane's
+        // 32-column x sum, (s0 + s1) + (s2 + s3)
+        const float s8 = quad_sum(i4_pair_sum_x(v));
         if (j == 0) s32[c * kWave + l] = s8;
-        // pair (x0,x2),(x4,x6),(x1,x3),(x5,x7) to match the nibble order of i4_word_dot
-        const u32x4 a = v;
-        v.x = (a.x & 0xFFFFu) | (a.y << 16);
-        v.y = (a.z & 0xFFFFu) | (a.w << 16);
-        v.z = (a.x >> 16) | (a.y & 0xFFFF0000u);
-        v.w = (a.z >> 16) | (a.w & 0xFFFF0000u);
     }
     xs[(c * XQ + j) * kWave + l] = v;
 }
@@ -132,12 +139,27 @@ __device__ __forceinline__ void x_store(const uint16_t* x, int K, int nchunks, c
     for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
 }
 
-// One item's registers: R*U weight loads, INT4 scales/zeros, and the (wave-uniform) position of the item.
-template <int F, int R, int U>
+// INT4 metadata per item (M = 1, U <= 4): lane 4j + i loads the scale (and zero point) of group 16*(c0 + i) + j, the
+// group quad j reads in the item's chunk i, so one load per row covers the item's U chunks; consume hands each
+// chunk's value to its quad with a DPP quad broadcast. Otherwise every lane loads its own group's metadata for
+// every chunk (one load per row and chunk).
+#ifndef PAIA_I4_QUAD_META
+#define PAIA_I4_QUAD_META 0
+#endif
+template <int F, int U, int MB>
+__host__ __device__ constexpr bool quad_meta()
+{
+    return PAIA_I4_QUAD_META && (F == kI4 || F == kI4ZP) && MB == 1 && U <= 4;
+}
+
+// One item's registers: R*U weight loads, INT4 scales/zeros, (XG) the lane's x vectors of its U chunks, and the
+// (wave-uniform) position of the item.
+template <int F, int R, int U, bool XG = false, bool QM = false>
 struct Item {
     u32x4 w[R][U];
-    uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) ? U : 1];
-    uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP ? U : 1];
+    u32x4 xg[XG ? U : 1][XG ? FmtInfo<F>::kXQ : 1];
+    uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) && !QM ? U : 1];
+    uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP && !QM ? U : 1];
     int group;           // row group (-1: no item)
     int chunk0;          // first chunk of the segment
     int k;               // index of the group in this wave's (H=0) or block's (H=1) sequence
@@ -178,16 +200,20 @@ struct ItemWalker {
 // The kernel body. MB activation rows (x [MB][K], y [MB][N]): MB = 1 is the M = 1 GEMV (gemv_kernel); MB = 2..6 (BF16, FP8:
 // 2..8) is the row-streaming small-batch kernel (gemv_rows_kernel): the same weight stream and decode, with MB
 // accumulators per row and MB staged copies of x, so each weight is loaded and decoded once for all activation rows.
-template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB>
+// XG: x is not staged; each item's loads bring the lane's x vectors from global memory (L2) with the weights. For K
+// whose staged x would not fit the LDS (M = 1 only).
+template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB, bool XG = false>
 __device__ __forceinline__ void gemv_body(const GemvParams& p)
 {
     static_assert(MB >= 1 && MB <= 8 && (MB <= 6 || F == kBF16 || F == kFP8) && (MB == 1 || !KSPLIT),
                   "activation rows: 1..6 (BF16, FP8 1..8), split-K only at M = 1");
+    static_assert(!XG || MB == 1, "x from global memory: M = 1 only");
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
+    constexpr bool QM = quad_meta<F, U, MB>();
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, then (H=1) the split-K partials
-    const uint32_t xrow = lds_x_bytes<F>(p.nchunks), srow = lds_s32_bytes<F>(p.nchunks);
+    const uint32_t xrow = XG ? 0u : lds_x_bytes<F>(p.nchunks), srow = XG ? 0u : lds_s32_bytes<F>(p.nchunks);
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
     float* s32 = reinterpret_cast<float*>(smem + MB * xrow);
     float* part = reinterpret_cast<float*>(smem + MB * xrow + MB * srow);
@@ -257,10 +283,12 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         ep_bias = ld_u16(make_rsrc(p.bias ? p.bias : p.x, p.bias ? (uint32_t)p.N * 2u : 0u), row * 2u, 0u);
     };
 
+    const __amdgpu_buffer_rsrc_t xrs_g = make_rsrc(p.x, XG ? (uint32_t)p.K * 2u : 0u);   // XG: x bounded to K
+
     // Loads of the item `it` points at into B (size-0 descriptors when there is none: no traffic). Every load is
     // issued unconditionally: a load under a branch would make the compiler wait for every outstanding load,
     // including the other buffer's, before using this item.
-    auto issue = [&](Item<F, R, U>& B) {
+    auto issue = [&](Item<F, R, U, XG, QM>& B) {
         const bool ok = it.valid();
         const int g = ok ? it.g : -1;
         if (g != bound_g) bind(g);
@@ -274,7 +302,18 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
-        if constexpr (I4) {
+        if constexpr (QM) {
+            // lane 4j + i: group 16*(chunk0 + i) + j (lanes i >= U load nothing: out-of-range offset)
+            const uint32_t i = (uint32_t)lane & 3u, j = (uint32_t)lane >> 2;
+            const uint32_t grp = 16u * ((uint32_t)B.chunk0 + i) + j;
+            const uint32_t moff = i < (uint32_t)U ? grp * 2u : kOOB;
+            const uint32_t zoff = i < (uint32_t)U ? grp >> 1 : kOOB;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                B.s[r][0] = ld_u16(rm[r], moff, 0u);
+                if constexpr (F == kI4ZP) B.z[r][0] = ld_u8(rz[r], zoff, 0u);
+            }
+        } else if constexpr (I4) {
             // the lane's 32 weights of chunk c lie in group c*16 + lane/4; zero points are packed 2 groups per byte
             const uint32_t moff = ((uint32_t)lane >> 2) * 2u + (uint32_t)B.chunk0 * 32u;
             const uint32_t zoff = ((uint32_t)lane >> 3) + (uint32_t)B.chunk0 * 8u;
@@ -285,6 +324,16 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
                     B.s[r][u] = ld_u16(rm[r], moff + (uint32_t)u * 32u, 0u);
                     if constexpr (F == kI4ZP) B.z[r][u] = ld_u8(rz[r], zoff + (uint32_t)u * 8u, 0u);
                 }
+        }
+        if constexpr (XG) {
+            // the lane's x for chunk c: columns c*CC + lane*CPL .. +CPL-1 (CPL = 8*XQ), XQ 16-byte vectors; bounded
+            // to K (zeros past it, and for no item at all)
+            constexpr uint32_t cpl = 8u * XQ, cc_bytes = 2u * kWave * cpl;
+            const uint32_t xoff = ok ? (uint32_t)B.chunk0 * cc_bytes + (uint32_t)lane * (2u * cpl) : kOOB;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int j = 0; j < XQ; ++j) B.xg[u][j] = ld16<0>(xrs_g, xoff + (uint32_t)u * cc_bytes + 16u * j, 0u);
         }
         it.advance();
     };
@@ -302,7 +351,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 
     // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
     // staged chunk so every product stays 0 * finite.
-    auto consume_rows = [&](const Item<F, R, U>& B) {
+    auto consume_rows = [&](const Item<F, R, U, XG, QM>& B) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int c = B.chunk0 + u;
@@ -372,26 +421,63 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         }
     };
 
-    auto consume = [&](const Item<F, R, U>& B) {
+    auto consume = [&](const Item<F, R, U, XG, QM>& B) {
         if constexpr (MB > 1) {
             consume_rows(B);
             return;
         }
+        // QM: each lane converts the metadata it loaded once per item (scale to f32, 128 + zero point); chunk u takes
+        // lane 4j + u's values by quad broadcast
+        float qs[QM ? R : 1], qzc[QM ? R : 1];
+        if constexpr (QM) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if constexpr (F == kI4) {
+                    qs[r] = f16_to_f32(B.s[r][0]);
+                    qzc[r] = 136.0f;                              // 128 (magic) + 8 (zero point)
+                } else {
+                    qs[r] = bf16_to_f32(B.s[r][0]);
+                    qzc[r] = 128.0f + (float)((B.z[r][0] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu);
+                }
+            }
+        }
+        auto quad_bcast_u = [&](int u, float v) {
+            return u == 0 ? quad_bcast<0>(v) : u == 1 ? quad_bcast<1>(v) : u == 2 ? quad_bcast<2>(v) : quad_bcast<3>(v);
+        };
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int c = B.chunk0 + u;
             c = c < nchunks ? c : nchunks - 1;
             u32x4 xv[XQ];
+            float sx_g = 0.0f;   // XG, INT4: the lane's 32-column x sum, in the staged order (s0 + s1) + (s2 + s3)
+            if constexpr (XG) {
+                float s8[XQ];
 #pragma unroll
-            for (int j = 0; j < XQ; ++j) xv[j] = xs[(c * XQ + j) * kWave + lane];
+                for (int j = 0; j < XQ; ++j) {
+                    xv[j] = B.xg[u][j];
+                    if constexpr (I4) s8[j] = i4_pair_sum_x(xv[j]);
+                }
+                if constexpr (I4) sx_g = (s8[0] + s8[1]) + (s8[2] + s8[3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < XQ; ++j) xv[j] = xs[(c * XQ + j) * kWave + lane];
+            }
             if constexpr (F == kBF16) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = dot_bf16_16B(B.w[r][u], xv[0], acc[r]);
             } else if constexpr (F == kFP8) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
+            } else if constexpr (QM) {
+                const float sx = XG ? sx_g : s32[c * kWave + lane];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
+                    const float s = quad_bcast_u(u, qs[r]), zc = quad_bcast_u(u, qzc[r]);
+                    acc[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, d), acc[r]);
+                }
             } else {
-                const float sx = s32[c * kWave + lane];
+                const float sx = XG ? sx_g : s32[c * kWave + lane];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
@@ -412,7 +498,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 
     // End of a group for this wave: reduce over the wave, then store (H=0) or park the partial in LDS (H=1).
     // MB > 1: reduce the R x MB sums (two per paired wave reduction), then lanes kk*R + r store row r's MB outputs
-    auto finish_rows = [&](const Item<F, R, U>& B) {
+    auto finish_rows = [&](const Item<F, R, U, XG, QM>& B) {
         constexpr int NV = R * MB;
         float flat[NV], tot[NV];
 #pragma unroll
@@ -445,7 +531,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         }
     };
 
-    auto finish = [&](const Item<F, R, U>& B) {
+    auto finish = [&](const Item<F, R, U, XG, QM>& B) {
         if constexpr (MB > 1) {
             finish_rows(B);
             return;
@@ -515,17 +601,21 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     constexpr int XE = MB == 1 ? XE0 : (XE0 / MB > 0 ? XE0 / MB : 1);
     constexpr int D = pipe_depth<R, U>();
     XRegs<XE> xr[MB];
+    if constexpr (!XG) {
 #pragma unroll
-    for (int m = 0; m < MB; ++m) x_load<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, xr[m]);
+        for (int m = 0; m < MB; ++m) x_load<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, xr[m]);
+    }
     if constexpr (!KSPLIT) ep_load(0);
-    Item<F, R, U> buf[D];
+    Item<F, R, U, XG, QM> buf[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(buf[d]);
+    if constexpr (!XG) {
 #pragma unroll
-    for (int m = 0; m < MB; ++m)
-        x_store<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xr[m], xs + m * xstride,
-                                  s32 + m * sstride);
-    __syncthreads();
+        for (int m = 0; m < MB; ++m)
+            x_store<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xr[m], xs + m * xstride,
+                                      s32 + m * sstride);
+        __syncthreads();
+    }
 
     // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
     // loop header without the other buffer's loads would make the compiler's wait counts assume those loads absent,
@@ -578,6 +668,13 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     gemv_body<F, R, U, W, AUX, KSPLIT, 1>(p);
 }
 
+// x from global memory (K beyond what the LDS can stage), M = 1.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+__global__ void __launch_bounds__(W * kWave) gemv_kernel_xg(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, KSPLIT, 1, true>(p);
+}
+
 // Small batch on the M = 1 design: MB = 2..6 (BF16 and FP8 2..8) activation rows, row-parallel (no split-K).
 template <int F, int R, int U, int W, int AUX, int MB>
 __global__ void __launch_bounds__(W * kWave) gemv_rows_kernel(GemvParams p)
@@ -618,9 +715,11 @@ constexpr uint32_t kPartBytes = 8192;
 template <int F, int R, int W, bool KSPLIT>
 uint32_t gemv_lds_plan(int nchunks, int* round)
 {
-    const uint32_t base = lds_x_bytes<F>(nchunks) + lds_s32_bytes<F>(nchunks);
     *round = 1;
-    if (base > kMaxLds) return 0;
+    // x plus INT4 sums: (XQ*1024 + 256) bytes per chunk; compared in 64 bits (nchunks reaches 2^22 at K = 2^31)
+    if ((uint64_t)nchunks * (FmtInfo<F>::kXQ * kChunkBytes + ((F == kI4 || F == kI4ZP) ? kWave * 4 : 0)) > kMaxLds)
+        return 0;
+    const uint32_t base = lds_x_bytes<F>(nchunks) + lds_s32_bytes<F>(nchunks);
     if (!KSPLIT) return base;
     const uint32_t group_bytes = (uint32_t)(W * R * 4);
     uint32_t part = kMaxLds - base < kPartBytes ? kMaxLds - base : kPartBytes;
@@ -698,7 +797,27 @@ int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
     return busiest_cu_groups(ng, even, W, cus) < busiest_cu_groups(ng, fewest, W, cus) ? even : fewest;
 }
 
-// Launch on `st`. Arguments were validated by the caller. Returns 0, -2 (LDS limit), or a hipError_t.
+// The launch for K whose staged x does not fit the LDS: x comes from global memory with each item's weights
+// (gemv_kernel_xg), split-K over the 8 waves of a block, one row per group, 2 KiB of each row per item; the LDS holds
+// only the split-K partials. Every variant of a format runs this kernel at such K (the knobs of the call are not
+// used), so any K the format's alignment rules accept runs. Returns 0 or a hipError_t.
+template <int F, int AUX>
+int launch_gemv_xg(GemvParams p, hipStream_t st)
+{
+    constexpr int R = 1, U = 2, W = 8;
+    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
+    p.nseg = (p.nchunks + U - 1) / U;
+    p.ngroups = (p.N + R - 1) / R;
+    p.round = (int)(kPartBytes / (uint32_t)(W * R * 4));
+    static std::atomic<int> cached{0};
+    const int per_cu = max_blocks_per_cu_of(gemv_kernel_xg<F, R, U, W, AUX, true>, W * kWave, cached);
+    const int grid = gemv_grid<R, W, true>(p, kPartBytes, per_cu);
+    hipLaunchKernelGGL((gemv_kernel_xg<F, R, U, W, AUX, true>), dim3(grid), dim3(W * kWave), kPartBytes, st, p);
+    return (int)hipGetLastError();
+}
+
+// Launch on `st`. Arguments were validated by the caller. Returns 0 or a hipError_t. K whose staged x (and, H=1, one
+// round of partials) does not fit the LDS runs launch_gemv_xg instead.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 int launch_gemv(GemvParams p, hipStream_t st)
 {
@@ -706,7 +825,7 @@ int launch_gemv(GemvParams p, hipStream_t st)
     p.nseg = (p.nchunks + U - 1) / U;
     p.ngroups = (p.N + R - 1) / R;
     const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
-    if (lds == 0) return -2;
+    if (lds == 0) return launch_gemv_xg<F, AUX>(p, st);
     const int grid = gemv_grid<R, W, KSPLIT>(p, lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>());
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();

@@ -13,6 +13,7 @@
 
 #include <cmath>
 
+#include "gemv_kernel.h"
 #include "paia_gemv.h"
 
 namespace {
@@ -27,6 +28,25 @@ const Pick kTuned[] = {
 #include "gemv_tuned.inc"
     {-1, 0, 0, 0, 0, 0, 0, 0},   // end marker
 };
+
+// Whether a variant of table 0 (BF16), 1 (FP8) or 2 (INT4) stages x for this K in the LDS: the launch's LDS plan
+// (paia::gemv_lds_plan) fits, x and the INT4 lane sums plus, for split-K, one round of partial sums. A variant that
+// does not runs the x-from-global kernel instead, which is slower, so the pick prefers one that does.
+bool stages_x(int table, int R, int W, int H, int K)
+{
+    using namespace paia;
+    const uint64_t row_bytes = table == 0 ? 2ull * (uint64_t)K : table == 1 ? (uint64_t)K : (uint64_t)K / 2u;
+    const uint64_t nchunks = (row_bytes + kChunkBytes - 1) / kChunkBytes;
+    const uint64_t xq = table == 0 ? 1u : table == 1 ? 2u : 4u;
+    const uint64_t base64 = nchunks * xq * kChunkBytes + (table == 2 ? nchunks * kWave * 4u : 0u);
+    if (base64 > kMaxLds) return false;
+    const uint32_t base = (uint32_t)base64;
+    if (!H) return true;
+    const uint32_t group = (uint32_t)(W * R * 4);
+    uint32_t part = kMaxLds - base < kPartBytes ? kMaxLds - base : kPartBytes;
+    part -= part % group;
+    return part >= group;
+}
 
 int find_bf16(int R, int U, int W, int S, int H)
 {
@@ -58,7 +78,9 @@ int paia_gemv_pick_variant(int kind, int N, int K)
 {
     if (kind < 0 || kind > 3) kind = 0;
     const int table = kind == 3 ? 2 : kind;   // both INT4 formats use the paia_gemv_int4 variant table
+    // a tuned entry counts only where its x fits the LDS at this K (a split-K entry needs room for its partials too)
     auto resolve = [&](const Pick& p) {
+        if (!stages_x(table, p.R, p.W, p.H, K)) return -1;
         return table == 0 ? find_bf16(p.R, p.U, p.W, p.S, p.H) : find_quant(table, p.R, p.U, p.W, p.H);
     };
     for (int pass = 0; pass < 2; ++pass) {    // this kind's row first; the asymmetric INT4 falls back to INT4's
@@ -87,10 +109,13 @@ int paia_gemv_pick_variant(int kind, int N, int K)
             if (best >= 0) return best;
         }
     }
-    int v = -1;
-    if (table == 0) v = find_bf16(2, 4, 4, 0, 1);
-    else if (table == 1) v = find_quant(1, 2, 2, 4, 1);
-    else v = find_quant(2, 4, 2, 4, 1);
+    // the harness default tuple, or its row-parallel twin where the split-K partials do not fit; at K beyond any
+    // staging, every variant runs the same x-from-global kernel
+    int R = 2, U = 4, W = 4, H = 1;
+    if (table == 1) U = 2;
+    else if (table == 2) R = 4, U = 2;
+    if (!stages_x(table, R, W, H, K)) H = 0;
+    const int v = table == 0 ? find_bf16(R, U, W, 0, H) : find_quant(table, R, U, W, H);
     return v < 0 ? 0 : v;
 }
 

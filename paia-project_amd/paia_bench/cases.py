@@ -70,8 +70,22 @@ class GemvCase:
     def _xshape(self):
         return (self.M, self.K) if self.mode == "batch" else (self.K,)
 
-    def build(self, n_copies: int, device="cuda", seed: int = 1234):
+    def build(self, n_copies: int, device="cuda", seed: int = 1234, host_copy0: bool = True):
+        """n_copies operand sets on the device. host_copy0: copy 0 = the seeded CPU operands (make_operands, the
+        ones `check` gates); otherwise every copy is drawn on the device (large shapes whose CPU generation would
+        dominate a benchmark run; gate copy 0 with check_copy, which builds its reference from device operands)."""
         dev = torch.device(device)
+        if not host_copy0:
+            assert self.mode != "batch", "device-only operands: M = 1 cases"
+            g = torch.Generator(device=dev).manual_seed(seed)
+            self.ops0 = None
+            self.copies = [self._random_copy(dev, g) for _ in range(n_copies)]
+            for c in self.copies:
+                c["y"] = torch.empty(self.N, dtype=torch.bfloat16, device=dev)
+            if self.mode == "unfused":
+                self.scratch = torch.empty(self.N * self.K, dtype=torch.bfloat16, device=dev)
+            self.ptrs = [self._ptrs(c) for c in self.copies]
+            return self
         self.ops0 = make_operands(self.fmt, self.N, self.K, bias=self.bias)
         if self.mode == "batch":
             # M activation rows: row 0 is the seeded x of make_operands, the others seeded after it
@@ -196,6 +210,45 @@ class GemvCase:
             refb = self._reference_row(self.ops0["x"].float(), idx, weights_bf16=True).to(torch.bfloat16).float()
         else:
             refb = ref.to(torch.bfloat16).float()
+        excess = ((y - refb).abs() - (atol + rtol * refb.abs())).max().item()
+        rel = ((y - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+        ok = bool(torch.isfinite(y).all().item()) and excess <= 0 and rel < 2e-2
+        return {"ok": ok, "rel_err": rel, "worst_excess": excess, "rows_checked": int(len(y))}
+
+    def copy_rows(self, i: int, rows) -> dict:
+        """The operands of copy i restricted to `rows` (M = 1 cases), as CPU torch tensors: what a CPU reference of
+        those output rows needs. Copies 1.. live only on the device, so this is how their outputs are checked."""
+        c = self.copies[i]
+        idx = torch.as_tensor(rows, dtype=torch.long, device=c["x"].device)
+        out = {"fmt": self.fmt, "N": len(rows), "K": self.K, "x": c["x"].cpu()}
+        for k in ("W", "Wq", "scale", "scales", "zeros", "bias"):
+            if c.get(k) is not None:
+                out[k] = c[k].index_select(0, idx).cpu()
+        return out
+
+    def reference_copy(self, i: int, rows) -> torch.Tensor:
+        """fp32 CPU reference of copy i's output rows (the harness method of `reference`, on that copy's operands)."""
+        o = self.copy_rows(i, rows)
+        if self.fmt == "bf16":
+            Wd = o["W"].float()
+        elif self.fmt == "fp8":
+            Wd = quant.dequant_fp8(o["Wq"], o["scale"])
+        elif self.fmt == "int4":
+            Wd = quant.dequant_int4(o["Wq"], o["scales"])
+        else:
+            Wd = quant.dequant_int4_zp(o["Wq"], o["scales"], o["zeros"])
+        ref = Wd @ o["x"].float()
+        if o.get("bias") is not None:
+            ref += o["bias"].float()
+        return ref
+
+    def check_copy(self, i: int, rows, rtol=1e-2, atol=1e-2) -> dict:
+        """Copy i's output as it stands (no launch: e.g. after a graph replay) against reference_copy, with the
+        gates of `check`."""
+        torch.cuda.synchronize()
+        y = self.copies[i]["y"].cpu().float()[torch.as_tensor(rows, dtype=torch.long)]
+        ref = self.reference_copy(i, rows)
+        refb = ref.to(torch.bfloat16).float()
         excess = ((y - refb).abs() - (atol + rtol * refb.abs())).max().item()
         rel = ((y - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
         ok = bool(torch.isfinite(y).all().item()) and excess <= 0 and rel < 2e-2

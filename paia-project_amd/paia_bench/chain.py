@@ -48,6 +48,21 @@ def build_chain(lib, fmt: str, model: str = "llama31_8b", layers: int = 32, devi
     return launches, total, checks
 
 
+def sample_rows(N: int, n: int = 64) -> list:
+    """n rows spread over [0, N), the first and the last included."""
+    return sorted(set(range(0, N, max(1, N // n))) | {N - 1})
+
+
+def check_layers(launches, layers, n_rows: int = 64) -> dict:
+    """After a replay: the outputs of the given layers (and of the lm_head) against the CPU fp32 reference built
+    from those layers' own device operands, on sampled rows. {case name@layer: check result}."""
+    out = {}
+    for case, i in launches:
+        if i in layers or case.name.startswith("bf16_lm_head"):
+            out[f"{case.name}@{i}"] = case.check_copy(i, sample_rows(case.N, n_rows))
+    return out
+
+
 def time_chain(launches, replays: int = 20, warmup: int = 3) -> dict:
     """One graph = one decode step's 129 launches; events around each replay on the launch stream."""
     def step():
@@ -70,16 +85,22 @@ def run_chain(lib, fmt: str, model: str = "llama31_8b", replays: int = 20, log=p
     if bad:
         raise RuntimeError(f"decode chain {fmt}: correctness gate failed: {bad}")
     t = time_chain(launches, replays)
+    # the outputs the replays left: layers 0, 1 and the last, and the lm_head, against their own operands
+    after = check_layers(launches, {0, 1, max(i for _, i in launches)})
+    bad = {k: v for k, v in after.items() if not v["ok"]}
+    if bad:
+        raise RuntimeError(f"decode chain {fmt}: outputs after the graph replays failed the gate: {bad}")
     gbps = total / (t["us_per_token_step"] * 1e-6) / 1e9
     log(f"  chain {fmt}: {t['us_per_token_step']:.1f} us/token-step, {gbps:.0f} GB/s over {total / 1e9:.2f} GB")
     res = {"format": fmt, "model": model, "bytes_per_step": total, "gbps": round(gbps, 1),
            "pct_of_8TBps": round(100 * gbps / 8000.0, 1), **{k: round(v, 2) if isinstance(v, float) else v
                                                              for k, v in t.items()},
-           "max_rel_err": max(v["rel_err"] for v in checks.values())}
+           "max_rel_err": max(v["rel_err"] for v in checks.values()),
+           "replayed_outputs_checked": sorted(after), "replayed_max_rel_err": max(v["rel_err"] for v in after.values())}
     for case in {c for c, _ in launches}:
         case.free()
     torch.cuda.empty_cache()
     return res
 
 
-__all__ = ["build_chain", "time_chain", "run_chain", "gemv_bytes"]
+__all__ = ["build_chain", "time_chain", "run_chain", "check_layers", "sample_rows", "gemv_bytes"]

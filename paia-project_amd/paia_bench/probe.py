@@ -2,8 +2,9 @@
 
     python -m paia_bench.probe [--out PATH]
 
-  * B0 (large): one 2 GiB nontemporal streaming read, best over grid sizes and unroll depths; the reference's dev B0
-    method (src/tests/gemv_bf16_check.cu:228-252) on MI355X.
+  * B0 (large): a 2 GiB nontemporal streaming read, best over two probes and their launch shapes (a grid-stride
+    loop, and the GEMV's own load path: raw buffer loads of 1-KiB chunks per wave from a persistent grid, two items
+    in flight); the reference's dev B0 method (src/tests/gemv_bf16_check.cu:228-252) on MI355X.
   * B0 at the GEMV sizes: reads of S bytes from distinct slices of a 2 GiB buffer, back to back in one graph (the
     same cold-cache rotation the GEMV timings use), so "us for S bytes" is the floor a GEMV of S bytes can reach.
   * launch floor: back-to-back empty kernels in one graph.
@@ -24,6 +25,9 @@ def load_probe():
     lib.paia_probe_read.restype = ctypes.c_int
     lib.paia_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_void_p]
+    lib.paia_probe_stream.restype = ctypes.c_int
+    lib.paia_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_void_p]
     lib.paia_probe_copy.restype = ctypes.c_int
     lib.paia_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
     lib.paia_probe_empty.restype = ctypes.c_int
@@ -31,53 +35,74 @@ def load_probe():
     return lib
 
 
-def b0_large(P, buf, sink, cus, configs=((2, 1), (2, 4), (2, 8), (4, 1), (4, 4), (4, 8), (8, 1), (8, 4), (8, 8),
-                                         (16, 1), (16, 4), (16, 8), (32, 1), (32, 4), (32, 8)), log=print):
-    """B0: the best streaming-read rate (GB/s) over (blocks per CU, unroll) configs, reading all of `buf` three times
-    per graph replay (median of 5 replays). Returns (GB/s, (blocks per CU, unroll))."""
+# Launch shapes of the two probes. ("gs", blocks per CU, unroll): the grid-stride loop of 256-thread blocks.
+# ("st", U, W, blocks per CU): the GEMV's load path (U 1-KiB chunks per item, W waves per block); at most 32 waves
+# per CU, as the GEMV's launches.
+GS_CONFIGS = [("gs", m, u) for m in (4, 8, 16) for u in (1, 4)]
+ST_CONFIGS = [("st", U, W, b) for U in (1, 2, 4, 8) for W, b in ((4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4),
+                                                                  (16, 1), (16, 2))]
+PROBE_CONFIGS = GS_CONFIGS + ST_CONFIGS
+
+
+def probe_launch(P, cfg, ptr, nbytes, sink_ptr, cus, stream):
+    """One read of nbytes at ptr with launch shape cfg (an entry of PROBE_CONFIGS)."""
+    if cfg[0] == "gs":
+        rc = P.paia_probe_read(ptr, nbytes, sink_ptr, cus * cfg[1], cfg[2], stream)
+    else:
+        rc = P.paia_probe_stream(ptr, nbytes, sink_ptr, cfg[1], cfg[2], cus * cfg[3], stream)
+    if rc:
+        raise RuntimeError(f"probe {cfg} rc {rc}")
+
+
+def b0_large(P, buf, sink, cus, configs=PROBE_CONFIGS, log=print):
+    """B0: the best streaming-read rate (GB/s) over the probes' launch shapes, reading all of `buf` (< 2 GiB) three
+    times per graph replay (median of 5 replays). Returns (GB/s, best config)."""
     from paia_gemv.loader import current_raw_stream
 
     from .timing import capture, replay_ms, stats
     total = buf.numel()
-
-    def read(grid, unroll):
-        rc = P.paia_probe_read(buf.data_ptr(), total, sink.data_ptr(), grid, unroll, current_raw_stream())
-        if rc:
-            raise RuntimeError(f"probe rc {rc}")
     best = (0.0, None)
-    for mult, unroll in configs:
-        g = capture(lambda: [read(cus * mult, unroll) for _ in range(3)], warm=1)
+    for cfg in configs:
+        g = capture(lambda: [probe_launch(P, cfg, buf.data_ptr(), total, sink.data_ptr(), cus, current_raw_stream())
+                             for _ in range(3)], warm=1)
         ms = stats(replay_ms(g, 5))["median"] / 3
         del g
         gbps = total / (ms * 1e-3) / 1e9
-        log(f"[b0] grid {cus}x{mult} unroll {unroll}: {gbps:.0f} GB/s")
+        log(f"[b0] {cfg}: {gbps:.0f} GB/s")
         if gbps > best[0]:
-            best = (gbps, (mult, unroll))
+            best = (gbps, cfg)
     return best
 
 
-def b0_sized(P, buf, sink, cus, S: int, mults=(4, 8, 16)) -> dict:
+def slice_plan(buf_bytes: int, S: int) -> tuple:
+    """(slice stride, number of slices) for reads of S bytes rotating over a buffer of buf_bytes: slices start every
+    stride bytes (S rounded up to 256) and every slice lies wholly inside the buffer. One slice when only one fits
+    (such a read is several times the 256 MiB last-level cache, so it cannot be served from it anyway)."""
+    if S <= 0 or S > buf_bytes:
+        raise ValueError(f"read of {S} bytes does not fit the {buf_bytes}-byte probe buffer")
+    stride = (S + 255) // 256 * 256
+    n = max(1, (buf_bytes - S) // stride + 1)
+    assert (n - 1) * stride + S <= buf_bytes
+    return stride, n
+
+
+def b0_sized(P, buf, sink, cus, S: int, configs=PROBE_CONFIGS) -> dict:
     """The read floor for S bytes: reads of S bytes from distinct slices of `buf`, back to back in one graph (the
-    GEMV timings' cold-cache rotation); the best µs per read over the grid sizes."""
+    GEMV timings' cold-cache rotation); the best µs per read over the probes' launch shapes."""
     from paia_gemv.loader import current_raw_stream
 
     from .timing import capture, replay_ms, stats
-    S16 = (S + 255) // 256 * 256
-    n = max(2, buf.numel() // S16)
+    S16, n = slice_plan(buf.numel(), S)
     R = min(2000, max(50, int(5e-3 / (S / 6e12))))
-
-    def read(ptr, grid):
-        rc = P.paia_probe_read(ptr, S, sink.data_ptr(), grid, 4, current_raw_stream())
-        if rc:
-            raise RuntimeError(f"probe rc {rc}")
     best = None
-    for mult in mults:
-        g = capture(lambda: [read(buf.data_ptr() + (j % n) * S16, cus * mult) for j in range(R)], warm=1)
-        us = stats(replay_ms(g, 5))["median"] * 1e3 / R
+    for cfg in configs:
+        g = capture(lambda: [probe_launch(P, cfg, buf.data_ptr() + (j % n) * S16, S, sink.data_ptr(), cus,
+                                          current_raw_stream()) for j in range(R)], warm=1)
+        us = stats(replay_ms(g, 3))["median"] * 1e3 / R
         del g
         if best is None or us < best[0]:
-            best = (us, mult)
-    return {"bytes": S, "us": best[0], "gbps": S / (best[0] * 1e-6) / 1e9, "grid_per_cu": best[1]}
+            best = (us, cfg)
+    return {"bytes": S, "us": best[0], "gbps": S / (best[0] * 1e-6) / 1e9, "cfg": list(best[1])}
 
 
 def main(argv=None):
@@ -94,7 +119,7 @@ def main(argv=None):
     P = load_probe()
     dev = torch.device("cuda:0")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    total = 2 * 2 ** 30
+    total = 2 * 2 ** 30 - 2 ** 20       # < 2 GiB: the GEMV-path probe's limit per launch
     buf = torch.empty(total, dtype=torch.uint8, device=dev)
     buf.random_(0, 255)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
@@ -103,7 +128,7 @@ def main(argv=None):
     # B0 large
     best = b0_large(P, buf, sink, cus, log=lambda m: print(m, flush=True))
     res["b0_gbps"] = best[0]
-    res["b0_cfg"] = {"grid_per_cu": best[1][0], "unroll": best[1][1]}
+    res["b0_cfg"] = list(best[1])
     print(f"[b0] best {best[0]:.0f} GB/s ({100 * best[0] / HBM_PEAK_GBPS:.1f}% of 8 TB/s) at {best[1]}", flush=True)
 
     # B0 at the GEMV sizes

@@ -5,7 +5,8 @@ Restates, step by step, the host-side launch sizing of `launch_gemv` and the dev
   * every weight chunk of every row is consumed exactly once (so every byte of W is read once),
   * every output row is stored exactly once,
   * split-K (H=1): every wave of a block reaches the same number of barriers, and LDS partial slots stay in range,
-  * the LDS request matches the -2 contract (x staging + INT4 sums + split-K partials <= 64 KiB).
+  * the LDS request fits (x staging + INT4 sums + split-K partials <= 64 KiB); K beyond that runs the
+    x-from-global launch (launch_gemv_xg: split-K, R=1, U=2, W=8, only the partials in LDS), replayed the same way.
 This is the gfx950 counterpart of the reference's index-logic replay (src/tests/emulate_mapping.py:10-66), re-derived
 for the wave64 item geometry. The constants below are the kernel's (kChunkBytes, kPartBytes, kMaxLds, FmtInfo::kXQ).
 """
@@ -54,14 +55,23 @@ def busiest_cu(ng, grid, W, cus):
     return max(load)
 
 
+XG_KNOBS = (1, 2, 8, 1)   # launch_gemv_xg: R, U, W, H
+
+
 def launch(fmt, N, K, R, U, W, H, cus, per_cu):
-    """Host sizing (launch_gemv): returns the params the kernel sees, or None for the -2 (LDS) case."""
+    """Host sizing (launch_gemv): the params the kernel sees. p["knobs"] are the (R, U, W, H) that run: the call's,
+    or launch_gemv_xg's when the staged x does not fit the LDS (p["xg"])."""
     rb = row_bytes(fmt, K)
     nchunks = -(-rb // CHUNK)
-    p = {"N": N, "rb": rb, "nchunks": nchunks, "nseg": -(-nchunks // U), "ngroups": -(-N // R)}
     lds, rnd = lds_plan(fmt, nchunks, R, W, H)
-    if lds == 0:
-        return None
+    xg = lds == 0
+    if xg:
+        R, U, W, H = XG_KNOBS
+        lds = PART_BYTES
+        rnd = PART_BYTES // (W * R * 4)
+        per_cu = min(per_cu, 4)      # 8-wave blocks: at most 32 waves per CU
+    p = {"N": N, "rb": rb, "nchunks": nchunks, "nseg": -(-nchunks // U), "ngroups": -(-N // R), "xg": xg,
+         "knobs": (R, U, W, H)}
     per_cu = min(per_cu, max(1, (160 * 1024) // lds))
     if W >= 16:
         per_cu = 1                   # a 16-wave block runs alone on its CU
@@ -99,8 +109,7 @@ def walk(p, block, wave, R, U, W, H):
 
 def replay(fmt, N, K, R, U, W, H, cus=256, per_cu=4):
     p = launch(fmt, N, K, R, U, W, H, cus, per_cu)
-    if p is None:
-        return None
+    R, U, W, H = p["knobs"]
     seen = {}                              # (group, chunk) -> count (chunks < nchunks only)
     stored = [0] * N
     for b in range(p["grid"]):
@@ -117,8 +126,8 @@ def replay(fmt, N, K, R, U, W, H, cus=256, per_cu=4):
                 for c in range(c0, c0 + U):
                     if c * CHUNK < p["rb"]:
                         seen[(g, c)] = seen.get((g, c), 0) + 1
-                    # x index clamp keeps LDS reads in range
-                    assert min(c, p["nchunks"] - 1) * XQ[fmt] * CHUNK < lds_bytes(fmt, p["nchunks"])
+                    # x index clamp keeps LDS reads in range (the x-from-global launch reads x bounded to K)
+                    assert p["xg"] or min(c, p["nchunks"] - 1) * XQ[fmt] * CHUNK < lds_bytes(fmt, p["nchunks"])
                 if last:
                     finished += 1
                     if not H:
@@ -177,24 +186,30 @@ def test_every_chunk_once_every_row_once(fmt):
 
 
 def test_real_shapes_grid_and_lds():
-    """Real BASELINE shapes on 256 CUs: the walk covers W exactly; the LDS request fits (no -2) for every format."""
+    """Real BASELINE shapes on 256 CUs: the walk covers W exactly; x is staged in the LDS (no fallback) for every
+    format."""
     shapes = [(6144, 4096), (4096, 4096), (4096, 14336), (3584, 3584), (3584, 18944), (4608, 3584)]
     for fmt, (N, K) in itertools.product(["bf16", "fp8", "int4zp"], shapes):
         for R, U, W, H in [(2, 2, 4, 0), (1, 4, 8, 1), (4, 1, 4, 0)]:
             if (R, U) not in {(r, u) for r, u, _, _ in KNOBS[fmt]}:
                 continue
-            assert replay(fmt, N, K, R, U, W, H, 256, 4) is not None
+            assert not replay(fmt, N, K, R, U, W, H, 256, 4)["xg"]
 
 
-def test_lds_limit_matches_contract():
-    """K beyond the LDS budget is rejected (-2), K at the documented maxima is accepted."""
-    assert launch("bf16", 8, 32768, 1, 1, 4, 0, 256, 1) is not None
-    assert launch("bf16", 8, 32776, 1, 1, 4, 0, 256, 1) is None
-    assert launch("bf16", 8, 32768, 1, 1, 4, 1, 256, 1) is None        # split-K needs room for one partial round
-    assert launch("bf16", 8, 32256, 4, 1, 8, 1, 256, 1) is not None
-    assert launch("fp8", 8, 32768, 1, 1, 4, 0, 256, 1) is not None
-    assert launch("int4", 8, 30720, 1, 1, 4, 0, 256, 1) is not None
-    assert launch("int4", 8, 30848, 1, 1, 4, 0, 256, 1) is None
+def test_lds_limit_and_the_x_from_global_launch():
+    """x is staged up to the documented maxima; beyond them (and, for split-K, where one round of partials no longer
+    fits beside x) the launch runs the x-from-global kernel, whose walk covers every chunk and row once."""
+    assert not launch("bf16", 8, 32768, 1, 1, 4, 0, 256, 1)["xg"]
+    assert launch("bf16", 8, 32776, 1, 1, 4, 0, 256, 1)["xg"]
+    assert launch("bf16", 8, 32768, 1, 1, 4, 1, 256, 1)["xg"]          # split-K needs room for one partial round
+    assert not launch("bf16", 8, 32256, 4, 1, 8, 1, 256, 1)["xg"]
+    assert not launch("fp8", 8, 32768, 1, 1, 4, 0, 256, 1)["xg"]
+    assert not launch("int4", 8, 30720, 1, 1, 4, 0, 256, 1)["xg"]
+    assert launch("int4", 8, 30848, 1, 1, 4, 0, 256, 1)["xg"]
+    for fmt, N, K in [("bf16", 33, 40000), ("bf16", 1, 65536 + 8), ("fp8", 129, 32784), ("fp8", 7, 100000),
+                      ("int4", 65, 30848), ("int4zp", 3, 65536 + 128)]:
+        for cus, per_cu in ((4, 2), (256, 4)):
+            assert replay(fmt, N, K, 2, 2, 4, 0, cus, per_cu)["xg"]
 
 
 def test_whole_blocks_per_cu_when_the_last_round_is_uneven():

@@ -90,15 +90,42 @@ def test_real_shapes_picked_and_default_variant(oracle, gemv_lib, cuda, fmt):
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4zp"])
 def test_bias_epilogue_qwen_qkv(oracle, gemv_lib, cuda, fmt):
-    """Qwen2.5 qkv 4608x3584 with the bf16 bias epilogue: y = bf16(acc + bias)."""
+    """Qwen2.5 qkv 4608x3584 with the bf16 bias epilogue: y = bf16(acc + bias), on every fifth
+    variant and always on the library's own pick for the shape (what a caller of variant -1 gets)."""
     N, K = 4608, 3584
     ops, np_ops = make(fmt, N, K, bias=True)
     dev = to_device(ops, cuda)
-    for v in variants(gemv_lib, fmt)[::5]:
-        note(f"bias {fmt} variant={v}")
-        y = run_gemv(gemv_lib, fmt, dev, v["id"])
+    ids = sorted({v["id"] for v in variants(gemv_lib, fmt)[::5]} | {gemv_lib.pick_variant(fmt, N, K)})
+    assert gemv_lib.pick_variant(fmt, N, K) in ids
+    for vid in ids:
+        note(f"bias {fmt} variant={vid}")
+        y = run_gemv(gemv_lib, fmt, dev, vid)
         torch.cuda.synchronize()
-        check(oracle, fmt, np_ops, y, f"bias {fmt} v{v}")
+        check(oracle, fmt, np_ops, y, f"bias {fmt} v{vid}")
+
+
+# K whose staged x does not fit the 64 KiB of LDS (BF16/FP8 K > 32768, INT4 K > 30720; split-K variants earlier):
+# the launch runs the x-from-global kernel whatever the variant. The reference accepts any K of the alignment rule
+# (src/paia_gemv/gemv_bf16.cu:50-51, gemv_quant.cu:66,75).
+BIG_K = {"bf16": [(33, 40000), (1, 65544), (64, 32768)], "fp8": [(129, 32784), (7, 100000)],
+         "int4": [(65, 30848), (3, 65664)], "int4zp": [(65, 30848), (3, 65664)]}
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4", "int4zp"])
+def test_k_beyond_lds_staging(oracle, gemv_lib, cuda, fmt):
+    """K beyond the LDS staging bound on the x-from-global kernel: the picked variant, a split-K and a row-parallel
+    variant (all run it) against the oracle, with bias where the format takes one."""
+    vs = variants(gemv_lib, fmt)
+    h1 = next(v["id"] for v in vs if (v["R"], v["U"], v["W"], v["H"]) == (2, 2, 4, 1))
+    h0 = next(v["id"] for v in vs if (v["R"], v["U"], v["W"], v["H"]) == (1, 1, 8, 0))
+    for N, K in BIG_K[fmt]:
+        ops, np_ops = make(fmt, N, K, bias=fmt != "int4")
+        dev = to_device(ops, cuda)
+        for vid in sorted({gemv_lib.pick_variant(fmt, N, K), h0, h1}):
+            note(f"big K {fmt} N={N} K={K} variant={vid}")
+            y = run_gemv(gemv_lib, fmt, dev, vid)
+            torch.cuda.synchronize()
+            check(oracle, fmt, np_ops, y, f"big K {fmt} {N}x{K} v{vid}")
 
 
 def column_dequant(O, fmt, np_ops, k):

@@ -126,3 +126,21 @@ def test_sweep_merge_writes_the_faster_cell(tmp_path):
     assert out["fp8_shapes"]["4096x4096"]["us"] == 4.0 and "1x2" in out["fp8_shapes"]
     assert out["fp8_batch_shapes"]["5x4096x4096"]["variant"] == rows
     assert "8x1x1" not in out["fp8_batch_shapes"]
+
+
+def test_probe_slices_stay_inside_the_buffer():
+    """The read-floor probe rotates reads of S bytes over slices of its buffer: every slice must lie wholly inside it,
+    for every GEMV of the benchmark (the 1.09 GB lm_heads leave room for one slice only), and a read larger than the
+    buffer is refused on the host."""
+    import bench
+    from paia_bench.probe import slice_plan
+    from paia_gemv.shapes import gemv_bytes
+    sizes = [gemv_bytes(f, N, K, b)["total"] for _, f, _, _, N, K, b in bench.PER_GEMV]
+    assert max(sizes) > bench.B0_BYTES // 2                      # the case that needs a single slice
+    for S in sizes + [1, 255, 256, 257, bench.B0_BYTES - 1, bench.B0_BYTES]:
+        stride, n = slice_plan(bench.B0_BYTES, S)
+        assert stride >= S and stride % 256 == 0 and n >= 1
+        assert (n - 1) * stride + S <= bench.B0_BYTES, (S, stride, n)
+    for S in (0, bench.B0_BYTES + 1):
+        with pytest.raises(ValueError):
+            slice_plan(bench.B0_BYTES, S)

@@ -93,9 +93,6 @@ def test_contract_return_codes_without_launch(gemv_lib):
     assert L.paia_quantize_int4_g128(A, A, A + 1, 4, 128, None) == -2         # scales not 2-byte aligned
     assert L.paia_quantize_int4_zp_g128(A, A, A, None, 4, 128, None) == -2    # zeros missing
     assert L.paia_quantize_int4_zp_g128(A, A, A, A, 0, 128, None) == -2       # N <= 0
-    # LDS limit of the gfx950 design: x is staged in 64 KiB
-    assert L.paia_gemv_bf16(A, A, A, 4, 32768 + 8, 0, None) == -2
-    assert L.paia_gemv_int4(A, A, A, A, 4, 30720 + 128, 0, None) == -2
 
 
 def test_python_surface_matches_reference(gemv_lib):
@@ -180,3 +177,35 @@ def test_untuned_shapes_take_the_nearest_tuned_entry(gemv_lib):
         n = {"bf16": L.n_variants, "fp8": len(L.variants_fp8)}.get(kind, len(L.variants_int4))
         for N, K in [(32, 4096), (300000, 4096), (1000, 30720), (8192, 8192)]:
             assert 0 <= L.pick_variant(kind, N, K) < n
+
+
+def _stages_x(fmt, R, W, H, K):
+    """The kernel's LDS plan (gemv_lds_plan): staged x + INT4 lane sums (+ one round of split-K partials) in 64 KiB."""
+    rb = {"bf16": 2 * K, "fp8": K}.get(fmt, K // 2)
+    nch = -(-rb // 1024)
+    base = nch * {"bf16": 1, "fp8": 2}.get(fmt, 4) * 1024 + (nch * 256 if fmt.startswith("int4") else 0)
+    if base > 65536:
+        return False
+    if not H:
+        return True
+    part = min(65536 - base, 8192)
+    part -= part % (W * R * 4)
+    return part >= W * R * 4
+
+
+def test_pick_variant_stages_x_up_to_the_staging_limit(gemv_lib):
+    """The picked variant stages x in the LDS for every K up to the largest staged K of its format, also where the
+    nearest tuned entry is a split-K variant whose partials would not fit beside x (BF16 64x32768, FP8 256x32768):
+    the pick then takes another entry or the default's row-parallel twin rather than the slower x-from-global
+    kernel."""
+    L = gemv_lib
+    kmax = {"bf16": 32768, "fp8": 32768, "int4": 30720, "int4zp": 30720}
+    step = {"bf16": 8, "fp8": 16, "int4": 128, "int4zp": 128}
+    for fmt in ("bf16", "fp8", "int4", "int4zp"):
+        table = {"bf16": L.variants, "fp8": L.variants_fp8}.get(fmt, L.variants_int4)
+        ks = sorted({k for k in range(step[fmt], kmax[fmt] + 1, 1024 * step[fmt] // 8)} |
+                    {kmax[fmt] - i * step[fmt] for i in range(0, 64)} | {4096, 14336, 18944, 3584})
+        for N in (32, 64, 256, 512, 4096, 128256):
+            for K in ks:
+                v = table[L.pick_variant(fmt, N, K)]
+                assert _stages_x(fmt, v["R"], v["W"], v["H"], K), (fmt, N, K, v)
