@@ -70,6 +70,16 @@ PAIA_API int paia_gemv_int4_naive(const void* Wq, const void* scales, const void
 PAIA_API int paia_gemv_int4_unfused(const void* Wq, const void* scales, const void* x, void* y, void* scratch_bf16,
                                     int N, int K, void* stream);
 
+/* No reference counterpart: for callers that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc), paia_gemv_int4_unfused without the caller's workspace. The dequantised
+ * bf16 rows go to a 32 MiB static device buffer of the library (one per GPU, held until the process ends), slice by
+ * slice of at most 32 MiB / (2K) rows (a multiple of 8), each slice's BF16 GEMV right after its dequantisation; the
+ * result equals paia_gemv_int4_unfused's bit for bit. Allocates nothing (the buffer's device address is looked up
+ * once per device, on the first call there). Returns -2 also when 8 rows do not fit the buffer (K > 2097152). Calls
+ * that overlap on one GPU (other streams, other threads) share the buffer and race: serialise them. */
+PAIA_API int paia_gemv_int4_unfused_noalloc(const void* Wq, const void* scales, const void* x, void* y, int N, int K,
+                                            void* stream);
+
 /* ---- INT4 W4A16 g128, asymmetric format (no reference counterpart; BASELINE INT4 configs): q in 0..15 packed as
  *      above, scales bf16 [N][G] (G = K/128), zeros [N][ceil(G/2)] bytes (group 2j low nibble, 2j+1 high nibble),
  *      dequant (q - z) * s; optional bias bf16 [N] (or NULL). Uses the paia_gemv_int4 variant table. --------- */

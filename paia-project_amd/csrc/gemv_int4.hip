@@ -15,6 +15,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "gemv_kernel.h"
 #include "paia_gemv.h"
 
@@ -126,6 +129,57 @@ int default_bf16_variant()
     return v;
 }
 
+// ---- the unfused control without a caller workspace (paia_gemv_int4_unfused_noalloc) ------------------------------
+// Scratch for the dequantised bf16 rows: a static device array (each GPU the library runs on holds its own copy from
+// module load to process exit). Host code never passes the array's name to a kernel (on the host it is only a
+// stand-in symbol): the device address comes from hipGetSymbolAddress, taken once per device with that device
+// current, on the entry point's first call there.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (0 and *rc = 0 on success, else *rc = the hipError_t or -2).
+void* scratch_device_ptr(int* rc)
+{
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *rc = (int)e;
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        *rc = -2;
+        return nullptr;
+    }
+    void* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_dev[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            const hipError_t g = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (g != hipSuccess || p == nullptr) {
+                *rc = g != hipSuccess ? (int)g : (int)hipErrorInvalidSymbol;
+                return nullptr;
+            }
+            g_scratch_dev[dev].store(p, std::memory_order_release);
+        }
+    }
+    *rc = 0;
+    return p;
+}
+
+// Rows per slice: as many whole 8-row blocks of bf16 rows as the scratch holds (8 keeps every slice's y and Wq
+// offsets 16-byte aligned). 0 when not even 8 rows fit (K > 2097152).
+int noalloc_slice_rows(int K)
+{
+    const size_t row = (size_t)K * 2u;
+    const size_t rows = kNoAllocScratchBytes / row;
+    return (int)(rows / 8u * 8u);
+}
+
 }  // namespace
 
 namespace paia {
@@ -194,6 +248,40 @@ int paia_gemv_int4_naive(const void* Wq, const void* scales, const void* x, void
                        static_cast<const uint8_t*>(Wq), static_cast<const uint16_t*>(scales),
                        static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), N, K);
     return (int)hipGetLastError();
+}
+
+int paia_gemv_int4_unfused_noalloc(const void* Wq, const void* scales, const void* x, void* y, int N, int K,
+                                   void* stream)
+{
+    if (N <= 0 || K <= 0 || (K & 127) || !aligned(Wq, 16) || !aligned(x, 16) || !aligned(scales, 2) ||
+        !aligned(y, 16))
+        return -2;
+    const int slice = noalloc_slice_rows(K);
+    if (slice < 8) return -2;   // K beyond the scratch: 8 bf16 rows of K values must fit kNoAllocScratchBytes
+    int rc = 0;
+    void* sp = scratch_device_ptr(&rc);
+    if (sp == nullptr) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int variant = default_bf16_variant();
+    const size_t wrow = (size_t)K / 2u, srow = (size_t)K / 128u;
+    // slice by slice on the caller's stream: dequantise rows [n0, n0 + n) into the scratch, then the BF16 GEMV of
+    // those rows into y[n0 ..]; the next slice's dequantisation is ordered after this GEMV, which has then read it.
+    // Each output row depends only on its own row and the variant, so the result equals paia_gemv_int4_unfused's.
+    for (int n0 = 0; n0 < N; n0 += slice) {
+        const int n = N - n0 < slice ? N - n0 : slice;
+        const size_t words = (size_t)n * (size_t)K / 8;
+        const size_t want = (words + 255) / 256;
+        const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+        hipLaunchKernelGGL(dequant_int4_bf16_kernel, dim3(grid), dim3(256), 0, st,
+                           static_cast<const uint8_t*>(Wq) + (size_t)n0 * wrow,
+                           static_cast<const uint16_t*>(scales) + (size_t)n0 * srow, static_cast<uint16_t*>(sp), words,
+                           K);
+        rc = (int)hipGetLastError();
+        if (rc) return rc;
+        rc = paia_gemv_bf16(sp, x, static_cast<uint16_t*>(y) + n0, n, K, variant, stream);
+        if (rc) return rc;
+    }
+    return 0;
 }
 
 int paia_gemv_int4_unfused(const void* Wq, const void* scales, const void* x, void* y, void* scratch_bf16, int N, int K,

@@ -56,6 +56,7 @@ class GemvLib:
             "paia_gemv_int4": [_P, _P, _P, _P, _I, _I, _I, _P],
             "paia_gemv_int4_naive": [_P, _P, _P, _P, _I, _I, _P],
             "paia_gemv_int4_unfused": [_P, _P, _P, _P, _P, _I, _I, _P],
+            "paia_gemv_int4_unfused_noalloc": [_P, _P, _P, _P, _I, _I, _P],
             "paia_gemv_int4_zp": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
             "paia_dequant_fp8": [_P, _P, _P, _I, _I, _P],
             "paia_dequant_int4": [_P, _P, _P, _I, _I, _P],
@@ -150,6 +151,12 @@ class GemvLib:
                                                      self._st(stream)), "paia_gemv_int4_unfused")
 
     # ---- gfx950 additions --------------------------------------------------------------------------------
+    def int4_unfused_noalloc(self, Wq_ptr, scales_ptr, x_ptr, y_ptr, N, K, stream=None):
+        """The unfused control without a workspace argument: the library's static device scratch (for callers that
+        cannot allocate; calls that overlap on one GPU race)."""
+        self._check(self._lib.paia_gemv_int4_unfused_noalloc(Wq_ptr, scales_ptr, x_ptr, y_ptr, N, K, self._st(stream)),
+                    "paia_gemv_int4_unfused_noalloc")
+
     def bf16_bias(self, W_ptr, x_ptr, bias_ptr, y_ptr, N, K, variant, stream=None):
         self._check(self._lib.paia_gemv_bf16_bias(W_ptr, x_ptr, bias_ptr, y_ptr, N, K, variant, self._st(stream)),
                     "paia_gemv_bf16_bias")
