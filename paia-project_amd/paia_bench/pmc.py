@@ -13,6 +13,13 @@ CAL_BYTES (reads CAL_BYTES, writes CAL_BYTES), then `reps` GEMVs of the named ca
 copies (>= 4 x 256 MiB) that every weight byte comes from HBM. FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in
 KiB per dispatch; `summarize` divides each by what the same counter read for the calibration kernels (bytes counted
 per byte moved), so `traffic` is in HBM bytes of the GEMV launch, next to its algorithmic bytes.
+
+Why FETCH_SIZE needs the calibration on MI355X: rocprofv3 defines it for gfx950 as (TCC_BUBBLE*128 + (TCC_EA0_RDREQ -
+TCC_BUBBLE - TCC_EA0_RDREQ_32B)*64 + TCC_EA0_RDREQ_32B*32) / 1024 KiB. On the read probe of 256 MiB, TCC_EA0_RDREQ
+counts 2^21 requests (one per 128 bytes) while TCC_BUBBLE, the 128-byte request count, reads 0: every request is
+weighed as 64 bytes, half its size, so FETCH_SIZE reads 0.5 byte per byte. An optional third pass of
+TCC_EA0_RDREQ_DRAM_32B_sum (32-byte units, a 128-byte request counting 4) measures the bytes read from HBM
+directly; it reads 1.0 per byte on the probe, with no calibration.
 """
 from __future__ import annotations
 
@@ -92,6 +99,7 @@ def cmd_summarize(a) -> int:
 
     fetch = _per_kernel(Path(a.fetch), "FETCH_SIZE")
     write = _per_kernel(Path(a.write), "WRITE_SIZE")
+    dram = _per_kernel(Path(a.dram), "TCC_EA0_RDREQ_DRAM_32B_sum") if a.dram else None
     kib = 1024.0
     cal_read = statistics.median(fetch["read_probe"]) * kib / CAL_BYTES          # counted bytes per byte read
     cal_copy_r = statistics.median(fetch["copy_probe"]) * kib / CAL_BYTES
@@ -109,9 +117,17 @@ def cmd_summarize(a) -> int:
                           "fetch_per_byte_copy_probe": round(cal_copy_r, 4),
                           "write_per_byte_copy_probe": round(cal_copy_w, 4)}
     alg = gemv_bytes(a.fmt, N, K, a.bias)["total"]
-    res.setdefault("cases", {})[a.case] = {
-        "kernel": k, "dispatches": len(fetch[k]), "fetch_bytes": round(fb), "write_bytes": round(wb),
-        "traffic_bytes": round(fb + wb), "algorithmic_bytes": alg, "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+    entry = {"kernel": k, "dispatches": len(fetch[k]), "fetch_bytes": round(fb), "write_bytes": round(wb),
+             "traffic_bytes": round(fb + wb), "algorithmic_bytes": alg,
+             "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+    if dram is not None:
+        # DRAM read requests in 32-byte units (a 128-byte request counts 4): bytes read from HBM, no calibration
+        cal_dram = statistics.median(dram["read_probe"]) * 32.0 / CAL_BYTES
+        res["calibration"]["dram32_bytes_per_byte_read_probe"] = round(cal_dram, 4)
+        db = statistics.median(dram[k]) * 32.0
+        entry["dram_read_bytes"] = round(db)
+        entry["dram_read_over_algorithmic"] = round(db / alg, 4)
+    res.setdefault("cases", {})[a.case] = entry
     out.parent.mkdir(parents=True, exist_ok=True)
     out.write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res["cases"][a.case] | {"calibration": res["calibration"]}, indent=1))
@@ -131,6 +147,7 @@ def main(argv=None) -> int:
     s = sub.add_parser("summarize")
     s.add_argument("--fetch", required=True)
     s.add_argument("--write", required=True)
+    s.add_argument("--dram", default=None, help="counter CSV of TCC_EA0_RDREQ_DRAM_32B_sum (optional)")
     s.add_argument("--out", required=True)
     s.add_argument("--case", required=True, help="name the entry is stored under (bench.py's case name)")
     s.add_argument("--fmt", default="fp8", choices=["bf16", "fp8", "int4", "int4zp"])
