@@ -140,7 +140,7 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     return (int)hipGetLastError();
 }
 
-// U in {1, 2, 4, 8}, W in {4, 8, 16}; grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
+// U in {1, 2, 4, 8} with W in {4, 8, 16}, and U = 16 with W in {4, 8}; grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
 __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, size_t nbytes, void* sink, int U, int W,
                                                              int grid, void* stream)
 {
@@ -152,7 +152,7 @@ __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, si
 #define PROBE_CASE(UU, WW) \
     if (U == UU && W == WW) return launch_stream<UU, WW>(buf, n, s, grid, st);
 #define PROBE_W(UU) PROBE_CASE(UU, 4) PROBE_CASE(UU, 8) PROBE_CASE(UU, 16)
-    PROBE_W(1) PROBE_W(2) PROBE_W(4) PROBE_W(8)
+    PROBE_W(1) PROBE_W(2) PROBE_W(4) PROBE_W(8) PROBE_CASE(16, 4) PROBE_CASE(16, 8)   // 16 KiB items at W = 16 spill
 #undef PROBE_W
 #undef PROBE_CASE
     return -1;

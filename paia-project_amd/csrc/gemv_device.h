@@ -198,13 +198,6 @@ __device__ __forceinline__ float wave_sum2(float a, float b)
     return v;
 }
 
-// Quad broadcast: every lane of quad q gets the value of lane 4q + I (DPP quad_perm [I,I,I,I]).
-template <int I>
-__device__ __forceinline__ float quad_bcast(float v)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), I * 0x55, 0xF, 0xF, false));
-}
-
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v)
 {

@@ -139,27 +139,14 @@ __device__ __forceinline__ void x_store(const uint16_t* x, int K, int nchunks, c
     for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
 }
 
-// INT4 metadata per item (M = 1, U <= 4): lane 4j + i loads the scale (and zero point) of group 16*(c0 + i) + j, the
-// group quad j reads in the item's chunk i, so one load per row covers the item's U chunks; consume hands each
-// chunk's value to its quad with a DPP quad broadcast. Otherwise every lane loads its own group's metadata for
-// every chunk (one load per row and chunk).
-#ifndef PAIA_I4_QUAD_META
-#define PAIA_I4_QUAD_META 0
-#endif
-template <int F, int U, int MB>
-__host__ __device__ constexpr bool quad_meta()
-{
-    return PAIA_I4_QUAD_META && (F == kI4 || F == kI4ZP) && MB == 1 && U <= 4;
-}
-
 // One item's registers: R*U weight loads, INT4 scales/zeros, (XG) the lane's x vectors of its U chunks, and the
 // (wave-uniform) position of the item.
-template <int F, int R, int U, bool XG = false, bool QM = false>
+template <int F, int R, int U, bool XG = false>
 struct Item {
     u32x4 w[R][U];
     u32x4 xg[XG ? U : 1][XG ? FmtInfo<F>::kXQ : 1];
-    uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) && !QM ? U : 1];
-    uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP && !QM ? U : 1];
+    uint32_t s[(F == kI4 || F == kI4ZP) ? R : 1][(F == kI4 || F == kI4ZP) ? U : 1];
+    uint32_t z[F == kI4ZP ? R : 1][F == kI4ZP ? U : 1];
     int group;           // row group (-1: no item)
     int chunk0;          // first chunk of the segment
     int k;               // index of the group in this wave's (H=0) or block's (H=1) sequence
@@ -210,7 +197,6 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     static_assert(!XG || MB == 1, "x from global memory: M = 1 only");
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
-    constexpr bool QM = quad_meta<F, U, MB>();
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, then (H=1) the split-K partials
     const uint32_t xrow = XG ? 0u : lds_x_bytes<F>(p.nchunks), srow = XG ? 0u : lds_s32_bytes<F>(p.nchunks);
@@ -288,7 +274,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     // Loads of the item `it` points at into B (size-0 descriptors when there is none: no traffic). Every load is
     // issued unconditionally: a load under a branch would make the compiler wait for every outstanding load,
     // including the other buffer's, before using this item.
-    auto issue = [&](Item<F, R, U, XG, QM>& B) {
+    auto issue = [&](Item<F, R, U, XG>& B) {
         const bool ok = it.valid();
         const int g = ok ? it.g : -1;
         if (g != bound_g) bind(g);
@@ -302,18 +288,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
-        if constexpr (QM) {
-            // lane 4j + i: group 16*(chunk0 + i) + j (lanes i >= U load nothing: out-of-range offset)
-            const uint32_t i = (uint32_t)lane & 3u, j = (uint32_t)lane >> 2;
-            const uint32_t grp = 16u * ((uint32_t)B.chunk0 + i) + j;
-            const uint32_t moff = i < (uint32_t)U ? grp * 2u : kOOB;
-            const uint32_t zoff = i < (uint32_t)U ? grp >> 1 : kOOB;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                B.s[r][0] = ld_u16(rm[r], moff, 0u);
-                if constexpr (F == kI4ZP) B.z[r][0] = ld_u8(rz[r], zoff, 0u);
-            }
-        } else if constexpr (I4) {
+        if constexpr (I4) {
             // the lane's 32 weights of chunk c lie in group c*16 + lane/4; zero points are packed 2 groups per byte
             const uint32_t moff = ((uint32_t)lane >> 2) * 2u + (uint32_t)B.chunk0 * 32u;
             const uint32_t zoff = ((uint32_t)lane >> 3) + (uint32_t)B.chunk0 * 8u;
@@ -351,7 +326,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 
     // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
     // staged chunk so every product stays 0 * finite.
-    auto consume_rows = [&](const Item<F, R, U, XG, QM>& B) {
+    auto consume_rows = [&](const Item<F, R, U, XG>& B) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int c = B.chunk0 + u;
@@ -421,29 +396,11 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         }
     };
 
-    auto consume = [&](const Item<F, R, U, XG, QM>& B) {
+    auto consume = [&](const Item<F, R, U, XG>& B) {
         if constexpr (MB > 1) {
             consume_rows(B);
             return;
         }
-        // QM: each lane converts the metadata it loaded once per item (scale to f32, 128 + zero point); chunk u takes
-        // lane 4j + u's values by quad broadcast
-        float qs[QM ? R : 1], qzc[QM ? R : 1];
-        if constexpr (QM) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if constexpr (F == kI4) {
-                    qs[r] = f16_to_f32(B.s[r][0]);
-                    qzc[r] = 136.0f;                              // 128 (magic) + 8 (zero point)
-                } else {
-                    qs[r] = bf16_to_f32(B.s[r][0]);
-                    qzc[r] = 128.0f + (float)((B.z[r][0] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu);
-                }
-            }
-        }
-        auto quad_bcast_u = [&](int u, float v) {
-            return u == 0 ? quad_bcast<0>(v) : u == 1 ? quad_bcast<1>(v) : u == 2 ? quad_bcast<2>(v) : quad_bcast<3>(v);
-        };
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int c = B.chunk0 + u;
@@ -468,14 +425,6 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
             } else if constexpr (F == kFP8) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
-            } else if constexpr (QM) {
-                const float sx = XG ? sx_g : s32[c * kWave + lane];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
-                    const float s = quad_bcast_u(u, qs[r]), zc = quad_bcast_u(u, qzc[r]);
-                    acc[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, d), acc[r]);
-                }
             } else {
                 const float sx = XG ? sx_g : s32[c * kWave + lane];
 #pragma unroll
@@ -498,7 +447,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 
     // End of a group for this wave: reduce over the wave, then store (H=0) or park the partial in LDS (H=1).
     // MB > 1: reduce the R x MB sums (two per paired wave reduction), then lanes kk*R + r store row r's MB outputs
-    auto finish_rows = [&](const Item<F, R, U, XG, QM>& B) {
+    auto finish_rows = [&](const Item<F, R, U, XG>& B) {
         constexpr int NV = R * MB;
         float flat[NV], tot[NV];
 #pragma unroll
@@ -531,7 +480,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         }
     };
 
-    auto finish = [&](const Item<F, R, U, XG, QM>& B) {
+    auto finish = [&](const Item<F, R, U, XG>& B) {
         if constexpr (MB > 1) {
             finish_rows(B);
             return;
@@ -606,7 +555,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         for (int m = 0; m < MB; ++m) x_load<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, xr[m]);
     }
     if constexpr (!KSPLIT) ep_load(0);
-    Item<F, R, U, XG, QM> buf[D];
+    Item<F, R, U, XG> buf[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(buf[d]);
     if constexpr (!XG) {
@@ -801,19 +750,25 @@ int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
 // (gemv_kernel_xg), split-K over the 8 waves of a block, one row per group, 2 KiB of each row per item; the LDS holds
 // only the split-K partials. Every variant of a format runs this kernel at such K (the knobs of the call are not
 // used), so any K the format's alignment rules accept runs. Returns 0 or a hipError_t.
-template <int F, int AUX>
-int launch_gemv_xg(GemvParams p, hipStream_t st)
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+int launch_gemv_xg_knobs(GemvParams p, hipStream_t st)
 {
-    constexpr int R = 1, U = 2, W = 8;
     p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
     p.nseg = (p.nchunks + U - 1) / U;
     p.ngroups = (p.N + R - 1) / R;
-    p.round = (int)(kPartBytes / (uint32_t)(W * R * 4));
+    p.round = KSPLIT ? (int)(kPartBytes / (uint32_t)(W * R * 4)) : 1;
+    const uint32_t lds = KSPLIT ? kPartBytes : 0u;
     static std::atomic<int> cached{0};
-    const int per_cu = max_blocks_per_cu_of(gemv_kernel_xg<F, R, U, W, AUX, true>, W * kWave, cached);
-    const int grid = gemv_grid<R, W, true>(p, kPartBytes, per_cu);
-    hipLaunchKernelGGL((gemv_kernel_xg<F, R, U, W, AUX, true>), dim3(grid), dim3(W * kWave), kPartBytes, st, p);
+    const int per_cu = max_blocks_per_cu_of(gemv_kernel_xg<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
+    const int grid = gemv_grid<R, W, KSPLIT>(p, lds, per_cu);
+    hipLaunchKernelGGL((gemv_kernel_xg<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();
+}
+
+template <int F, int AUX>
+int launch_gemv_xg(GemvParams p, hipStream_t st)
+{
+    return launch_gemv_xg_knobs<F, 1, 2, 8, AUX, true>(p, st);
 }
 
 // Launch on `st`. Arguments were validated by the caller. Returns 0 or a hipError_t. K whose staged x (and, H=1, one

@@ -39,9 +39,13 @@ def load_probe():
 # ("st", U, W, blocks per CU): the GEMV's load path (U 1-KiB chunks per item, W waves per block); at most 32 waves
 # per CU, as the GEMV's launches.
 GS_CONFIGS = [("gs", m, u) for m in (4, 8, 16) for u in (1, 4)]
-ST_CONFIGS = [("st", U, W, b) for U in (1, 2, 4, 8) for W, b in ((4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4),
-                                                                  (16, 1), (16, 2))]
+ST_CONFIGS = [("st", U, W, b) for U in (1, 2, 4, 8, 16) for W, b in ((4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4),
+                                                                      (16, 1), (16, 2)) if U < 16 or W < 16]
 PROBE_CONFIGS = GS_CONFIGS + ST_CONFIGS
+# the read floor at a GEMV's byte count sweeps a subset (every grid-stride shape, the GEMV-path probe at every item
+# size on the four launch shapes the GEMVs use most)
+SIZED_CONFIGS = GS_CONFIGS + [("st", U, W, b) for U in (1, 2, 4, 8, 16) for W, b in ((4, 8), (8, 2), (8, 4), (16, 1))
+                              if U < 16 or W < 16]
 
 
 def probe_launch(P, cfg, ptr, nbytes, sink_ptr, cus, stream):
@@ -86,7 +90,7 @@ def slice_plan(buf_bytes: int, S: int) -> tuple:
     return stride, n
 
 
-def b0_sized(P, buf, sink, cus, S: int, configs=PROBE_CONFIGS) -> dict:
+def b0_sized(P, buf, sink, cus, S: int, configs=SIZED_CONFIGS) -> dict:
     """The read floor for S bytes: reads of S bytes from distinct slices of `buf`, back to back in one graph (the
     GEMV timings' cold-cache rotation); the best µs per read over the probes' launch shapes."""
     from paia_gemv.loader import current_raw_stream

@@ -43,7 +43,7 @@ KINDS = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}
 
 
 class GemvLib:
-    CODES = "-1 bad variant, -2 bad shape/alignment, >0 hipError_t"
+    CODES = "-1: no such variant; -2: shape or alignment outside the contract; > 0: HIP error"
 
     def __init__(self, path=None):
         self.path = path or find_lib()
@@ -118,7 +118,7 @@ class GemvLib:
     @classmethod
     def _check(cls, rc, what):
         if rc != 0:
-            raise RuntimeError(f"{what} failed with code {rc} ({cls.CODES})")
+            raise RuntimeError(f"{what} returned {rc} ({cls.CODES})")
 
     @staticmethod
     def _st(stream):
@@ -126,19 +126,23 @@ class GemvLib:
 
     # ---- reference surface -------------------------------------------------------------------------------
     def bf16(self, W_ptr, x_ptr, y_ptr, N, K, variant, stream=None):
-        """y[N] = W[N,K] @ x[K]; pointers are ints. Raises on a nonzero return code."""
+        """BF16 weights: the output vector (N bf16 values) from the row-major N x K matrix and the K-vector, each
+        passed as a device address (int)."""
         rc = self._fn(W_ptr, x_ptr, y_ptr, N, K, variant, self._st(stream))
         if rc != 0:
-            raise RuntimeError(f"paia_gemv_bf16 failed with code {rc} (N={N}, K={K}, variant={variant}); "
-                               "-1 bad variant, -2 bad shape/alignment (K%8, 16B pointers), >0 hipError_t")
+            raise RuntimeError(f"paia_gemv_bf16 returned {rc} for N={N} K={K} variant {variant} "
+                               "(-1: no such variant; -2: K not a multiple of 8 or a pointer not 16-byte aligned; "
+                               "> 0: HIP error)")
 
     def fp8(self, Wq_ptr, scale_ptr, x_ptr, y_ptr, N, K, variant, stream=None):
-        """Wq [N,K] e4m3 bytes, scale [N] fp32, x [K] bf16, y [N] bf16; K % 16 == 0."""
+        """FP8 weights: one e4m3fn byte per weight (N x K), one fp32 scale per output row; bf16 x and y; K a
+        multiple of 16."""
         self._check(self._lib.paia_gemv_fp8(Wq_ptr, scale_ptr, x_ptr, y_ptr, N, K, variant, self._st(stream)),
                     "paia_gemv_fp8")
 
     def int4(self, Wq_ptr, scales_ptr, x_ptr, y_ptr, N, K, variant, stream=None):
-        """Wq [N,K/2] packed, scales [N,K/128] fp16; K % 128 == 0. Fused kernel."""
+        """INT4 weights, two per byte (N x K/2), zero point 8, one fp16 scale per 128 columns of a row; K a multiple
+        of 128. The fused kernel."""
         self._check(self._lib.paia_gemv_int4(Wq_ptr, scales_ptr, x_ptr, y_ptr, N, K, variant, self._st(stream)),
                     "paia_gemv_int4")
 

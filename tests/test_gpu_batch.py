@@ -109,7 +109,7 @@ def test_every_variant_awkward_shapes(oracle, gemv_lib, cuda, fmt):
                 if not runs(fmt, M, N, K, v, rows_lds_limit()):
                     # S*M*U too large for the LDS chunk, or a row-streaming variant of another M: the entry point
                     # refuses it (-2) before launching
-                    with pytest.raises(RuntimeError, match="code -2"):
+                    with pytest.raises(RuntimeError, match="returned -2"):
                         run_batch(gemv_lib, fmt, dev, xd, v["id"])
                     continue
                 note(f"batch {fmt} M={M} N={N} K={K} variant={v}")
@@ -137,7 +137,7 @@ def test_row_streaming_variants_awkward_shapes(oracle, gemv_lib, cuda, fmt):
             xd = x.to(cuda)
             for v in rows_vs:
                 if not runs(fmt, M, N, K, v, rows_lds_limit()):
-                    with pytest.raises(RuntimeError, match="code -2"):
+                    with pytest.raises(RuntimeError, match="returned -2"):
                         run_batch(gemv_lib, fmt, dev, xd, v["id"])
                     continue
                 note(f"rows {fmt} M={M} N={N} K={K} variant={v}")
