@@ -140,10 +140,15 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     return (int)hipGetLastError();
 }
 
-// U in {1, 2, 4, 8} with W in {4, 8, 16}, and U = 16 with W in {4, 8}; grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
+// U in {1, 2, 4, 8} with W in {4, 8, 16}, U = 16 with W in {4, 8}, and U in {8, 16} with W = 1 (one-wave blocks: the
+// walk of a split-K GEMV launch whose rows are one segment long, where one wave per block streams whole row pairs);
+// grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
 __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, size_t nbytes, void* sink, int U, int W,
                                                              int grid, void* stream)
 {
+    const bool shape_ok = ((U == 1 || U == 2 || U == 4 || U == 8) && (W == 4 || W == 8 || W == 16)) ||
+                          (U == 16 && (W == 4 || W == 8)) || ((U == 8 || U == 16) && W == 1);
+    if (!shape_ok) return -1;   // checked first, so a caller can test a shape with null buffers
     if (!buf || !sink || (reinterpret_cast<uintptr_t>(buf) & 15) || grid <= 0 || nbytes == 0 || nbytes >= (1ull << 31))
         return -2;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -153,6 +158,7 @@ __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, si
     if (U == UU && W == WW) return launch_stream<UU, WW>(buf, n, s, grid, st);
 #define PROBE_W(UU) PROBE_CASE(UU, 4) PROBE_CASE(UU, 8) PROBE_CASE(UU, 16)
     PROBE_W(1) PROBE_W(2) PROBE_W(4) PROBE_W(8) PROBE_CASE(16, 4) PROBE_CASE(16, 8)   // 16 KiB items at W = 16 spill
+    PROBE_CASE(8, 1) PROBE_CASE(16, 1)
 #undef PROBE_W
 #undef PROBE_CASE
     return -1;

@@ -36,8 +36,6 @@
 
 namespace paia {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTileRows = 16;    // weight rows per MFMA tile
 constexpr int kBlockCols = 128;  // columns per k-block (4 MFMA steps of 32; one INT4 group)

@@ -10,7 +10,9 @@
 namespace paia {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------------------------------------
 // weight formats
@@ -159,6 +161,54 @@ __device__ __forceinline__ float dot_i4_16B(const u32x4 w, const u32x4 x0, const
     d = i4_word_dot(w.z, x2, d, c43);
     d = i4_word_dot(w.w, x3, d, c43);
     return d;
+}
+
+// INT4 as bf16 subnormals (the decode of the kernels that stage x in LDS). Bits 0-7 of a bf16 whose high byte is 0
+// hold any byte b as exactly b * 2^-133: b < 128 is the subnormal b * 2^-133, b >= 128 has exponent field 1 and
+// mantissa b - 128, i.e. (1 + (b-128)/128) * 2^-126. So a nibble masked in place is q * 2^-133 in bits 0-3 and
+// 16 q * 2^-133 in bits 4-7, and v_dot2_f32_bf16 takes subnormal operands as they are (measured on gfx950, as does
+// the bf16 MFMA). With x staged as x * 2^64 against bits 0-3 and x * 2^60 against bits 4-7 every product is exactly
+// q x 2^-69 (12 significant bits), so the dot of a word is 2^-69 sum q x with no offset to remove: 5 VALU (two masks,
+// one shift, two masks) + 4 v_dot2 per 8 weights, where the 0x43-exponent decode takes 7 + 4 and leaves a
+// 128 sum x term. The pairs are (q0,q4), (16q1,16q5), (q2,q6), (16q3,16q7) against x staged as
+// (x0,x4)2^64, (x1,x5)2^60, (x2,x6)2^64, (x3,x7)2^60. Exact while |x| < 2^64 (x * 2^64 stays finite) and the
+// products stay normal (|q x| >= 2^-57); outside that range an x overflows to inf or a product loses bits.
+constexpr int kI4DnXLog2 = 64;             // x scale against a nibble in bits 0-3 (bits 4-7: 2^60)
+constexpr float kI4DnUnit = 0x1p-69f;      // the dot products come out in units of 2^-69
+constexpr float kI4DnOut = 0x1p69f;        // ... so each output row is scaled back once, after its reduction
+__device__ __forceinline__ void i4_word_decode_dn(uint32_t w, uint32_t q4[4])
+{
+    const uint32_t t = w >> 8;
+    q4[0] = w & 0x000F000Fu;   // (q0, q4)
+    q4[1] = w & 0x00F000F0u;   // (16 q1, 16 q5)
+    q4[2] = t & 0x000F000Fu;   // (q2, q6)
+    q4[3] = t & 0x00F000F0u;   // (16 q3, 16 q7)
+}
+__device__ __forceinline__ float i4dn_word_dot(uint32_t w, const u32x4 x, float acc)
+{
+    uint32_t q4[4];
+    i4_word_decode_dn(w, q4);
+    acc = dot2_bf16(q4[0], x.x, acc);
+    acc = dot2_bf16(q4[1], x.y, acc);
+    acc = dot2_bf16(q4[2], x.z, acc);
+    acc = dot2_bf16(q4[3], x.w, acc);
+    return acc;
+}
+__device__ __forceinline__ float dot_i4dn_16B(const u32x4 w, const u32x4 x0, const u32x4 x1, const u32x4 x2,
+                                              const u32x4 x3)
+{
+    float d = i4dn_word_dot(w.x, x0, 0.0f);
+    d = i4dn_word_dot(w.y, x1, d);
+    d = i4dn_word_dot(w.z, x2, d);
+    d = i4dn_word_dot(w.w, x3, d);
+    return d;
+}
+
+// Two floats -> one bf16 pair (v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+    const bf16x2 r = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -16,13 +16,14 @@
 //     per-wave partial sums go to LDS and are combined in a fixed order after a block barrier (one barrier per round
 //     of up to `round` groups, not per group). This is the split-K used for tall-K / small-N shapes.
 //   * x is staged once per block into LDS, already in the pairing each format's dot product wants (natural bf16
-//     pairs for BF16/FP8; (k, k+4) pairs for INT4) plus, for INT4, the sum of each lane's 32 x values. The first
-//     two items' weight loads are issued before the staging, so their latency overlaps it.
+//     pairs for BF16/FP8; (k, k+4) pairs scaled by 2^64 / 2^60 for INT4) plus, for INT4, the sum of each lane's 32
+//     x values. The first two items' weight loads are issued before the staging, so their latency overlaps it.
 //   * Weight rows are read with raw buffer loads through one descriptor per row group; a lane whose 16 bytes lie past
 //     the row end (K tails, padding segments, rows >= N) gets an out-of-range offset and reads zeros without a branch
 //     or any memory traffic.
 //   * Dequantisation happens in registers: FP8 via the gfx950 OCP e4m3 -> f32 convert packed to bf16, INT4 by
-//     masking nibbles into the mantissa of bf16 128.0; every product is a v_dot2 bf16 with fp32 accumulation.
+//     masking nibbles in place as bf16 subnormals (q * 2^-133, against x scaled by 2^64; the x-from-global kernel
+//     masks them into the mantissa of bf16 128.0 instead); every product is a v_dot2 bf16 with fp32 accumulation.
 //
 // No MFMA: at M=1 the arithmetic intensity is ~1-4 FLOP/byte and the kernel is HBM-bound.
 #pragma once
@@ -90,8 +91,8 @@ __device__ __forceinline__ void x_load(const uint16_t* x, int K, XRegs<XE>& xr)
     for (int e = 0; e < XE; ++e) xr.v[e] = ld16<0>(xrs, ((uint32_t)threadIdx.x + (uint32_t)(e * NT)) * 16u, 0u);
 }
 
-// INT4: the sum of one x vector's 8 values (fixed order), and the vector re-paired (x0,x2),(x4,x6),(x1,x3),(x5,x7)
-// to match the nibble order of i4_word_dot.
+// INT4, x read from global memory (the x-from-global kernel): the sum of one x vector's 8 values (fixed order), and
+// the vector re-paired (x0,x2),(x4,x6),(x1,x3),(x5,x7) to match the nibble order of i4_word_dot.
 __device__ __forceinline__ float i4_pair_sum_x(u32x4& v)
 {
     const float s8 = ((bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16)) +
@@ -106,6 +107,24 @@ __device__ __forceinline__ float i4_pair_sum_x(u32x4& v)
     return s8;
 }
 
+// INT4, staged x for the subnormal decode (i4_word_decode_dn): the sum of the vector's 8 values (same fixed order as
+// i4_pair_sum_x), and the vector re-paired (x0,x4),(x1,x5),(x2,x6),(x3,x7) with pairs 0 and 2 scaled by 2^64 and
+// pairs 1 and 3 by 2^60 (exact: a power-of-two scale of a bf16 is a bf16 unless it overflows).
+__device__ __forceinline__ float i4_stage_x(u32x4& v)
+{
+    const float f[8] = {bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                        bf16_to_f32(v.y >> 16),     bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16),
+                        bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16)};
+    const float s8 = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+    constexpr float a = 0x1p64f, b = 0x1p60f;
+    static_assert(kI4DnXLog2 == 64, "staging scales follow the decode's");
+    v.x = pack_bf16x2(f[0] * a, f[4] * a);
+    v.y = pack_bf16x2(f[1] * b, f[5] * b);
+    v.z = pack_bf16x2(f[2] * a, f[6] * a);
+    v.w = pack_bf16x2(f[3] * b, f[7] * b);
+    return s8;
+}
+
 template <int F>
 __device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
 {
@@ -114,9 +133,9 @@ __device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
     const int l = r / XQ, j = r - l * XQ;
     if constexpr (F == kI4 || F == kI4ZP) {
         // the 4 vectors of a lane-segment are 4 consecutive q in one quad of threads: the quad sum is the lane's
-        // 32-column x sum, (s0 + s1) + (s2 + s3)
-        const float s8 = quad_sum(i4_pair_sum_x(v));
-        if (j == 0) s32[c * kWave + l] = s8;
+        // 32-column x sum, (s0 + s1) + (s2 + s3), kept in the decode's units of 2^-69
+        const float s8 = quad_sum(i4_stage_x(v));
+        if (j == 0) s32[c * kWave + l] = s8 * kI4DnUnit;
     }
     xs[(c * XQ + j) * kWave + l] = v;
 }
@@ -207,6 +226,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     const int lane = lane_id();
     const int wave = wave_id();
     const uint32_t lane16 = (uint32_t)lane * 16u;
+    const uint32_t gl = (uint32_t)lane >> 2;   // INT4: the lane's 32 weights lie in group gl of the chunk
     // INT4 decode constant, made opaque so it stays in one register instead of a literal per instruction
     const uint32_t c43 = (uint32_t)__builtin_amdgcn_readfirstlane(0x43434343);
     const uint32_t row_bytes = p.row_bytes;
@@ -289,9 +309,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 #pragma unroll
             for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
         if constexpr (I4) {
-            // the lane's 32 weights of chunk c lie in group c*16 + lane/4; zero points are packed 2 groups per byte
-            const uint32_t moff = ((uint32_t)lane >> 2) * 2u + (uint32_t)B.chunk0 * 32u;
-            const uint32_t zoff = ((uint32_t)lane >> 3) + (uint32_t)B.chunk0 * 8u;
+            // the lane's 32 weights of chunk c lie in group c*16 + gl; zero points are packed 2 groups per byte
+            const uint32_t moff = gl * 2u + (uint32_t)B.chunk0 * 32u;
+            const uint32_t zoff = (gl >> 1) + (uint32_t)B.chunk0 * 8u;
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -365,9 +385,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 #pragma unroll
                     for (int m = 0; m < MB; ++m) dm[m] = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {   // word i: 8 nibbles -> 4 bf16 pairs (128 + q), then MB dot chains
+                    for (int i = 0; i < 4; ++i) {   // word i: 8 nibbles -> 4 bf16 subnormal pairs, then MB dot chains
                         uint32_t q4[4];
-                        i4_word_decode(ww[i], c43, q4);
+                        i4_word_decode_dn(ww[i], q4);
 #pragma unroll
                         for (int m = 0; m < MB; ++m) {
                             const u32x4 xw = xv[m][i];
@@ -380,11 +400,10 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
                     float s, zc;
                     if constexpr (F == kI4) {
                         s = f16_to_f32(B.s[r][u]);
-                        zc = 136.0f;                              // 128 (magic) + 8 (zero point)
+                        zc = 8.0f;                                // the format's zero point
                     } else {
                         s = bf16_to_f32(B.s[r][u]);
-                        const uint32_t z = (B.z[r][u] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu;
-                        zc = 128.0f + (float)z;
+                        zc = (float)((B.z[r][u] >> (gl & 1u) * 4u) & 0xFu);
                     }
 #pragma unroll
                     for (int m = 0; m < MB; ++m) {
@@ -426,18 +445,22 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
             } else {
+                // staged x: the subnormal decode, dot and x sum in units of 2^-69, no decode offset; XG: the
+                // 0x43-exponent decode against unscaled x, offset 128
                 const float sx = XG ? sx_g : s32[c * kWave + lane];
+                constexpr float off = XG ? 128.0f : 0.0f;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float d = dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
+                    const float d = XG ? dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43)
+                                       : dot_i4dn_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3]);
                     float s, zc;
                     if constexpr (F == kI4) {
                         s = f16_to_f32(B.s[r][u]);
-                        zc = 136.0f;                              // 128 (magic) + 8 (zero point)
+                        zc = off + 8.0f;                          // decode offset + the format's zero point
                     } else {
                         s = bf16_to_f32(B.s[r][u]);
-                        const uint32_t z = (B.z[r][u] >> (((uint32_t)lane >> 2) & 1u) * 4u) & 0xFu;
-                        zc = 128.0f + (float)z;
+                        const uint32_t z = (B.z[r][u] >> (gl & 1u) * 4u) & 0xFu;
+                        zc = off + (float)z;
                     }
                     acc[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, sx, d), acc[r]);
                 }
@@ -464,6 +487,10 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
             tot[i + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
         }
         if constexpr (NV & 1) tot[NV - 1] = wave_sum(flat[NV - 1]);
+        if constexpr (I4) {   // the subnormal decode's units, 2^-69 (exact: a power of two)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) tot[i] *= kI4DnOut;
+        }
         const int kk = B.k;
         const int r = lane - kk * R;
         const int row = B.group * R + r;
@@ -493,6 +520,10 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
             tot[r + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
         }
         if constexpr (R & 1) tot[R - 1] = wave_sum(acc[R - 1]);
+        if constexpr (I4 && !XG) {   // the subnormal decode's units, 2^-69 (exact: a power of two)
+#pragma unroll
+            for (int r = 0; r < R; ++r) tot[r] *= kI4DnOut;
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
         if constexpr (!KSPLIT) {

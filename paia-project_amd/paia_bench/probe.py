@@ -37,15 +37,18 @@ def load_probe():
 
 # Launch shapes of the two probes. ("gs", blocks per CU, unroll): the grid-stride loop of 256-thread blocks.
 # ("st", U, W, blocks per CU): the GEMV's load path (U 1-KiB chunks per item, W waves per block); at most 32 waves
-# per CU, as the GEMV's launches.
+# per CU, as the GEMV's launches. One-wave blocks of 8 or 16 KiB items, 4 or 8 per CU, follow a split-K GEMV whose
+# rows are one segment long (the BF16 lm_head 128256x4096 at R=2, U=8: one wave per block streams 16 KiB row pairs,
+# consecutive pairs on consecutive blocks).
 GS_CONFIGS = [("gs", m, u) for m in (4, 8, 16) for u in (1, 4)]
+ONE_WAVE_CONFIGS = [("st", U, 1, b) for U in (8, 16) for b in (4, 8)]
 ST_CONFIGS = [("st", U, W, b) for U in (1, 2, 4, 8, 16) for W, b in ((4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4),
                                                                       (16, 1), (16, 2)) if U < 16 or W < 16]
-PROBE_CONFIGS = GS_CONFIGS + ST_CONFIGS
+PROBE_CONFIGS = GS_CONFIGS + ST_CONFIGS + ONE_WAVE_CONFIGS
 # the read floor at a GEMV's byte count sweeps a subset (every grid-stride shape, the GEMV-path probe at every item
-# size on the four launch shapes the GEMVs use most)
+# size on the four launch shapes the GEMVs use most, and the one-wave blocks)
 SIZED_CONFIGS = GS_CONFIGS + [("st", U, W, b) for U in (1, 2, 4, 8, 16) for W, b in ((4, 8), (8, 2), (8, 4), (16, 1))
-                              if U < 16 or W < 16]
+                              if U < 16 or W < 16] + ONE_WAVE_CONFIGS
 
 
 def probe_launch(P, cfg, ptr, nbytes, sink_ptr, cus, stream):

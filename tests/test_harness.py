@@ -144,3 +144,15 @@ def test_probe_slices_stay_inside_the_buffer():
     for S in (0, bench.B0_BYTES + 1):
         with pytest.raises(ValueError):
             slice_plan(bench.B0_BYTES, S)
+
+
+def test_every_probe_shape_is_instantiated():
+    """Each GEMV-path probe shape the benchmark sweeps is one the probe library launches: the entry point rejects an
+    unknown (U, W) with -1 before looking at its buffers, so null buffers tell the two apart without a GPU (-2)."""
+    from paia_bench.probe import PROBE_CONFIGS, SIZED_CONFIGS, load_probe
+    P = load_probe()
+    for cfg in set(PROBE_CONFIGS) | set(SIZED_CONFIGS):
+        if cfg[0] == "st":
+            assert P.paia_probe_stream(None, 1 << 20, None, cfg[1], cfg[2], 256 * cfg[3], None) == -2, cfg
+    assert P.paia_probe_stream(None, 1 << 20, None, 16, 16, 256, None) == -1       # spills: not instantiated
+    assert P.paia_probe_stream(None, 1 << 20, None, 4, 1, 256, None) == -1
