@@ -9,6 +9,8 @@
 //   persistent grid of blocks_per_cu blocks of W waves on every CU (the walk of the fused GEMV at R = 1, H = 0,
 //   without x, the decode or the store). The benchmark takes the best of both probes, over their launch shapes, as
 //   the read floor.
+// paia_probe_stream_lead: the same read in 8-wave blocks of which only wave 0 streams (items dealt round-robin to the
+//   blocks), the walk of a split-K GEMV launch whose rows are one segment long.
 // paia_probe_copy: a plain 16-byte-per-lane copy of known size, the calibration kernel for the rocprofv3 byte counters
 //   (FETCH_SIZE should read its size once, WRITE_SIZE its size once).
 // paia_probe_empty: an empty kernel, for the per-launch floor of back-to-back launches in a graph.
@@ -51,17 +53,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // traffic). The loop is left by `return` when a wave's items run out, as the GEMV's loop is. The loads come from
 // read-only memory, so the compiler may move them to their first use (then only one item is in flight): an empty
 // asm barrier after each issue keeps them in place, and the exit folds both buffers (zeros there) into the sink.
-template <int U, int W>
+// LEAD: only wave 0 of each block streams, taking items blockIdx.x + k*gridDim.x; the other waves return at once.
+template <int U, int W, bool LEAD>
 __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __restrict__ buf, uint32_t nbytes,
                                                               uint32_t* sink)
 {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(buf, nbytes);
     const uint32_t lane16 = (threadIdx.x & 63u) * 16u;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (LEAD && wave != 0) return;
     constexpr uint32_t item_bytes = U * 1024u;
     const uint32_t nitems = (nbytes + item_bytes - 1) / item_bytes;
-    uint32_t item = blockIdx.x * W + wave;
-    const uint32_t stride = gridDim.x * W;
+    uint32_t item = LEAD ? blockIdx.x : blockIdx.x * W + wave;
+    const uint32_t stride = LEAD ? gridDim.x : gridDim.x * W;
     uint32_t acc = 0;
     u32x4 b[2][U];
     bool valid[2];
@@ -102,10 +106,10 @@ __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __rest
     }
 }
 
-template <int U, int W>
+template <int U, int W, bool LEAD = false>
 int launch_stream(const void* buf, uint32_t nbytes, uint32_t* sink, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((stream_probe_kernel<U, W>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink);
+    hipLaunchKernelGGL((stream_probe_kernel<U, W, LEAD>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink);
     return (int)hipGetLastError();
 }
 
@@ -140,14 +144,13 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     return (int)hipGetLastError();
 }
 
-// U in {1, 2, 4, 8} with W in {4, 8, 16}, U = 16 with W in {4, 8}, and U in {8, 16} with W = 1 (one-wave blocks: the
-// walk of a split-K GEMV launch whose rows are one segment long, where one wave per block streams whole row pairs);
-// grid = blocks (the caller passes CUs x blocks per CU); nbytes < 2^31.
+// U in {1, 2, 4, 8} with W in {4, 8, 16}, and U = 16 with W in {4, 8}; grid = blocks (the caller passes CUs x blocks
+// per CU); nbytes < 2^31.
 __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, size_t nbytes, void* sink, int U, int W,
                                                              int grid, void* stream)
 {
     const bool shape_ok = ((U == 1 || U == 2 || U == 4 || U == 8) && (W == 4 || W == 8 || W == 16)) ||
-                          (U == 16 && (W == 4 || W == 8)) || ((U == 8 || U == 16) && W == 1);
+                          (U == 16 && (W == 4 || W == 8));
     if (!shape_ok) return -1;   // checked first, so a caller can test a shape with null buffers
     if (!buf || !sink || (reinterpret_cast<uintptr_t>(buf) & 15) || grid <= 0 || nbytes == 0 || nbytes >= (1ull << 31))
         return -2;
@@ -158,10 +161,22 @@ __attribute__((visibility("default"))) int paia_probe_stream(const void* buf, si
     if (U == UU && W == WW) return launch_stream<UU, WW>(buf, n, s, grid, st);
 #define PROBE_W(UU) PROBE_CASE(UU, 4) PROBE_CASE(UU, 8) PROBE_CASE(UU, 16)
     PROBE_W(1) PROBE_W(2) PROBE_W(4) PROBE_W(8) PROBE_CASE(16, 4) PROBE_CASE(16, 8)   // 16 KiB items at W = 16 spill
-    PROBE_CASE(8, 1) PROBE_CASE(16, 1)
 #undef PROBE_W
 #undef PROBE_CASE
     return -1;
+}
+
+// 8-wave blocks whose wave 0 streams U-KiB items (U in {8, 16}); grid = blocks; nbytes < 2^31.
+__attribute__((visibility("default"))) int paia_probe_stream_lead(const void* buf, size_t nbytes, void* sink, int U,
+                                                                  int grid, void* stream)
+{
+    if (U != 8 && U != 16) return -1;   // checked first, so a caller can test a shape with null buffers
+    if (!buf || !sink || (reinterpret_cast<uintptr_t>(buf) & 15) || grid <= 0 || nbytes == 0 || nbytes >= (1ull << 31))
+        return -2;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* s = static_cast<uint32_t*>(sink);
+    const uint32_t n = (uint32_t)nbytes;
+    return U == 8 ? launch_stream<8, 8, true>(buf, n, s, grid, st) : launch_stream<16, 8, true>(buf, n, s, grid, st);
 }
 
 __attribute__((visibility("default"))) int paia_probe_copy(const void* src, void* dst, size_t nbytes, int grid,

@@ -7,8 +7,8 @@
 //   * Work unit ("item"): R consecutive rows x one K-segment of U 1-KiB chunks. A wave reads a chunk of a row with one
 //     16-byte buffer load per lane (64 lanes x 16 B = 1 KiB), so an item is R*U loads.
 //   * Each wave walks its own sequence of items and keeps the next item's loads in flight while it consumes the
-//     current one (two register buffers, both filled while x is staged). There is no block-wide synchronisation in the streaming loop, so the memory
-//     pipeline never drains at row-group boundaries.
+//     current one (two register buffers, both filled while x is staged). There is no block-wide synchronisation in
+//     the streaming loop, so the memory pipeline never drains at row-group boundaries.
 //   * H=0: a wave owns whole row groups (all segments of a group are consecutive items of one wave; the partial sums
 //     stay in registers). Groups are dealt to the waves of the grid round-robin, so at any moment the grid streams a
 //     window of neighbouring rows.
@@ -750,8 +750,21 @@ inline int busiest_cu_groups(int ng, int grid, int W, int cus)
 // rounds: a whole number of blocks on every CU when that lowers the busiest CU's groups (the fewest blocks covering N
 // in q rounds leave some CUs a block more than others: BF16 gate_up 28672x4096 at 3.5 blocks per CU took 38.5 µs,
 // at 4 blocks per CU 35.2).
+// Split-K launches whose rows are one segment long (U KiB covers a whole row: the lm_heads at U = 8 in BF16) leave
+// every wave but the first of a block without a segment, so one wave per block streams whole row groups. For BF16
+// (a bare v_dot2 per 4 bytes of weights) 2 such blocks per CU stream fastest: on MI355X, BF16 lm_head 152064x3584 at
+// R=1 U=8 W=4 takes 153.1 µs at 2 blocks per CU, 158.6 at 4; 128256x4096 at R=2 U=8 W=8 144.1 and 144.6 (a read
+// probe of the walk: 143-147 µs per 1.05-1.09 GB at 2, 144-149 at 4). The FP8 and INT4 decodes cost more per byte
+// and want more one-wave blocks per CU (FP8 128256x4096 at R=1 U=4 W=4: 74.9 µs at 4, 129.7 at 2), so they keep the
+// general sizing.
+#ifndef PAIA_GEMV_LEAD_WAVE_BLOCKS_PER_CU
+#define PAIA_GEMV_LEAD_WAVE_BLOCKS_PER_CU 2
+#endif
+constexpr int kLeadWaveBlocksPerCu = PAIA_GEMV_LEAD_WAVE_BLOCKS_PER_CU;
+
+// lead_cap: blocks per CU for a one-segment split-K launch (0: no cap).
 template <int R, int W, bool KSPLIT>
-int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
+int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu, int lead_cap = 0)
 {
     const DeviceFacts df = device_facts();
     if (df.lds_per_cu > 0) {
@@ -759,6 +772,7 @@ int gemv_grid(const GemvParams& p, uint32_t lds, int per_cu)
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
     }
     if (per_cu > max_blocks_per_cu_for<W>()) per_cu = max_blocks_per_cu_for<W>();
+    if (KSPLIT && p.nseg == 1 && lead_cap > 0 && per_cu > lead_cap) per_cu = lead_cap;
     const int cus = df.cus > 0 ? df.cus : 256;
     const int gmax = cus * per_cu;
     const int ng = p.ngroups;
@@ -812,7 +826,8 @@ int launch_gemv(GemvParams p, hipStream_t st)
     p.ngroups = (p.N + R - 1) / R;
     const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
     if (lds == 0) return launch_gemv_xg<F, AUX>(p, st);
-    const int grid = gemv_grid<R, W, KSPLIT>(p, lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>());
+    const int grid = gemv_grid<R, W, KSPLIT>(p, lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>(),
+                                             F == kBF16 ? kLeadWaveBlocksPerCu : 0);
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();
 }

@@ -75,6 +75,8 @@ def launch(fmt, N, K, R, U, W, H, cus, per_cu):
     per_cu = min(per_cu, max(1, (160 * 1024) // lds))
     if W >= 16:
         per_cu = 1                   # a 16-wave block runs alone on its CU
+    if H and p["nseg"] == 1 and fmt == "bf16" and not xg:
+        per_cu = min(per_cu, 2)      # BF16, one segment per row: one streaming wave per block, 2 blocks per CU
     gmax = cus * per_cu
     unit = 1 if H else W
     ng = p["ngroups"]
@@ -234,3 +236,14 @@ def test_groups_per_wave_capped_for_the_epilogue_register():
     not fit the one register loaded before the streaming loop); the launch grows the grid instead."""
     for R, U, W in [(1, 1, 4), (2, 2, 4), (4, 1, 8), (8, 1, 4)]:
         replay("fp8", 40000, 256, R, U, W, 0, cus=2, per_cu=1)
+
+
+def test_one_segment_split_k_runs_two_blocks_per_cu():
+    """BF16 split-K with rows one segment long (the lm_heads at U = 8): one wave per block streams, the launch holds
+    at most 2 blocks per CU, and the walk still covers every row once. Other formats keep the general sizing."""
+    for N, K in [(128256, 4096), (152064, 3584)]:
+        p = launch("bf16", N, K, 2, 8, 8, 1, 256, 4)
+        assert p["nseg"] == 1 and p["grid"] <= 2 * 256
+        replay("bf16", N // 64, K, 2, 8, 8, 1, 256, 4)     # coverage on a smaller N with the same walk
+    assert launch("bf16", 128256, 4096, 2, 4, 8, 1, 256, 4)["grid"] > 2 * 256   # two segments: unchanged
+    assert launch("fp8", 128256, 4096, 1, 4, 4, 1, 256, 8)["grid"] > 2 * 256    # FP8: general sizing

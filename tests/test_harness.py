@@ -154,5 +154,8 @@ def test_every_probe_shape_is_instantiated():
     for cfg in set(PROBE_CONFIGS) | set(SIZED_CONFIGS):
         if cfg[0] == "st":
             assert P.paia_probe_stream(None, 1 << 20, None, cfg[1], cfg[2], 256 * cfg[3], None) == -2, cfg
+        elif cfg[0] == "lw":
+            assert P.paia_probe_stream_lead(None, 1 << 20, None, cfg[1], 256 * cfg[2], None) == -2, cfg
     assert P.paia_probe_stream(None, 1 << 20, None, 16, 16, 256, None) == -1       # spills: not instantiated
     assert P.paia_probe_stream(None, 1 << 20, None, 4, 1, 256, None) == -1
+    assert P.paia_probe_stream_lead(None, 1 << 20, None, 4, 256, None) == -1
