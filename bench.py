@@ -23,8 +23,9 @@ Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmi
                 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/pmc_traffic.json), calibrated on kernels
                 of known size. roofline_by_dtype: the same for each format's dominant Llama GEMV
   b0            the streaming-read probe in the same run (the reference's measured-bandwidth denominator "B0"): the
-                best rate of a 2 GiB (less 1 MiB) read, and the read floor for each GEMV's byte count under the same cold-cache
-                rotation; per_gemv then also carries % of B0 and the GEMV time over that floor (skipped with --no-b0)
+                best rate of a 2 GiB (less 1 MiB) read, and for each GEMV's byte count under the same cold-cache
+                rotation the read floor and the I/O floor (the same reads also writing the GEMV's N bf16 outputs);
+                per_gemv then also carries % of B0 and the GEMV time over both floors (skipped with --no-b0)
   chain         BASELINE configs[4]: 32 layers x 4 GEMVs + bf16 lm_head as one hipGraph, INT4 (asymmetric g128) and
                 FP8: us per token-step and aggregate GB/s; layer 0 gated before capture, layers 0, 1, 31 and the head
                 after the replays (skipped with --no-chain)
@@ -76,11 +77,12 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def measure_b0(dev, cases, per: dict) -> dict:
+def measure_b0(dev, cases, per: dict, log=lambda m: None) -> dict:
     """B0 (the reference's measured streaming-read bandwidth, src/tests/gemv_bf16_check.cu:228-252) in this run: the
-    best rate of a 2 GiB (less 1 MiB) read over the probe's launch shapes, then, for each GEMV case, the read floor for its byte
-    count (reads of that size rotating over the 2 GiB buffer, back to back in one graph). Adds pct_of_b0 and
-    over_read_floor (GEMV µs / floor µs) to each per_gemv entry."""
+    best rate of a 2 GiB (less 1 MiB) read over the probe's launch shapes, then, for each GEMV case (name, bytes, N),
+    the read floor for its byte count (reads of that size rotating over the 2 GiB buffer, back to back in one graph)
+    and the I/O floor (the same reads that also write the GEMV's N bf16 outputs). Adds pct_of_b0, over_read_floor and
+    over_io_floor (GEMV µs / floor µs) to each per_gemv entry."""
     import torch
     from paia_bench.probe import b0_large, b0_sized, load_probe
 
@@ -90,14 +92,18 @@ def measure_b0(dev, cases, per: dict) -> dict:
     buf.random_(0, 255)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     gbps, cfg = b0_large(P, buf, sink, cus, log=lambda m: None)
+    y = torch.empty(max(n for _, _, n in cases), dtype=torch.bfloat16, device=dev)
     sized = {}
-    for name, nbytes in cases:
-        r = b0_sized(P, buf, sink, cus, nbytes)
-        sized[name] = {"bytes": r["bytes"], "us": round(r["us"], 3), "gbps": round(r["gbps"], 1), "cfg": r["cfg"]}
+    for name, nbytes, nout in cases:
+        r = b0_sized(P, buf, sink, cus, nbytes, y=y, nout=nout)
+        sized[name] = {"bytes": r["bytes"], "us": round(r["us"], 3), "gbps": round(r["gbps"], 1), "cfg": r["cfg"],
+                       "io_us": round(r["io_us"], 3), "io_cfg": r["io_cfg"], "nout": nout}
         e = per[name]
         e["pct_of_b0"] = round(100 * e["gbps"] / gbps, 1)
         e["over_read_floor"] = round(e["us"] / r["us"], 3)
-    del buf
+        e["over_io_floor"] = round(e["us"] / r["io_us"], 3)
+        log(f"  {name}: read floor {r['us']:.2f} us {r['cfg']}, I/O floor {r['io_us']:.2f} us {r['io_cfg']}")
+    del buf, y
     torch.cuda.empty_cache()
     return {"gbps": round(gbps, 1), "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "bytes": B0_BYTES,
             "cfg": cfg, "read_floor": sized}
@@ -243,7 +249,7 @@ def measure_per_gemv(lib, dev) -> dict:
         torch.cuda.empty_cache()
         gbps = c.bytes()["total"] / (t["us"] * 1e-6) / 1e9
         fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
-        per[name] = {"config": cfg, "us": round(t["us"], 3), "gbps": round(gbps, 1),
+        per[name] = {"config": cfg, "N": N, "K": K, "us": round(t["us"], 3), "gbps": round(gbps, 1),
                      "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "variant": fam[c.variant],
                      "kernel": kernel_name(lib, fmt, c.variant), "bytes": c.bytes()["total"], "R": t["R"],
                      "copies": n_rot, "rel_err": round(chk["rel_err"], 5)}
@@ -341,7 +347,7 @@ def main(argv=None):
         by_dtype = {f: roofline_entry(lib, n, per[n]) for f, n in DOMINANT.items()}
         if not a.no_b0:
             log("streaming-read probe (B0) ...")
-            b0 = measure_b0(dev, [(n, e["bytes"]) for n, e in per.items()], per)
+            b0 = measure_b0(dev, [(n, e["bytes"], e["N"]) for n, e in per.items()], per, log=log)
             log(f"  b0 {b0['gbps']:.0f} GB/s ({b0['pct_of_8TBps']:.1f}% of 8 TB/s)")
 
     chain = None

@@ -11,6 +11,10 @@
 //   the read floor.
 // paia_probe_stream_lead: the same read in 8-wave blocks of which only wave 0 streams (items dealt round-robin to the
 //   blocks), the walk of a split-K GEMV launch whose rows are one segment long.
+// paia_probe_set_output: makes the read probes also write a GEMV's output, nout bf16 values (0: none, the default),
+//   each thread or wave its equal share when its reads are done (the cheapest time to write them: a GEMV that writes
+//   a row group's outputs as the group completes cannot do better). The benchmark's "I/O floor" of a GEMV: its
+//   weight bytes read and its outputs written.
 // paia_probe_copy: a plain 16-byte-per-lane copy of known size, the calibration kernel for the rocprofv3 byte counters
 //   (FETCH_SIZE should read its size once, WRITE_SIZE its size once).
 // paia_probe_empty: an empty kernel, for the per-launch floor of back-to-back launches in a graph.
@@ -21,8 +25,9 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-template <int UNROLL>
-__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict__ p, size_t n16, uint32_t* sink)
+template <int UNROLL, bool OUT>
+__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict__ p, size_t n16, uint32_t* sink,
+                                                         uint16_t* y, uint32_t nout)
 {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -39,6 +44,8 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads from being removed
+    if (OUT)
+        for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < nout; j += stride) y[j] = (uint16_t)acc;
 }
 
 constexpr uint32_t kOOB = 0x80000000u;
@@ -54,9 +61,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // read-only memory, so the compiler may move them to their first use (then only one item is in flight): an empty
 // asm barrier after each issue keeps them in place, and the exit folds both buffers (zeros there) into the sink.
 // LEAD: only wave 0 of each block streams, taking items blockIdx.x + k*gridDim.x; the other waves return at once.
-template <int U, int W, bool LEAD>
+// OUT: streaming wave gw of nw writes outputs [gw*nout/nw, (gw+1)*nout/nw) when its items are done.
+template <int U, int W, bool LEAD, bool OUT>
 __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __restrict__ buf, uint32_t nbytes,
-                                                              uint32_t* sink)
+                                                              uint32_t* sink, uint16_t* y, uint32_t nout)
 {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(buf, nbytes);
     const uint32_t lane16 = (threadIdx.x & 63u) * 16u;
@@ -79,6 +87,7 @@ __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __rest
         item += stride;
         asm volatile("" ::: "memory");   // compiler barrier: the loads stay where they are issued (no sinking)
     };
+    const uint32_t first = item;   // the wave's index among the streaming waves (its first item)
     auto consume = [&](int d) {
 #pragma unroll
         for (int u = 0; u < U; ++u) acc ^= b[d][u].x ^ b[d][u].y ^ b[d][u].z ^ b[d][u].w;
@@ -93,6 +102,11 @@ __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __rest
             consume(0);
             consume(1);
             if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads alive
+            if (OUT) {
+                const uint32_t o1 = (uint32_t)((uint64_t)(first + 1) * nout / stride);
+                for (uint32_t o = (uint32_t)((uint64_t)first * nout / stride) + (threadIdx.x & 63u); o < o1; o += 64u)
+                    y[o] = (uint16_t)acc;
+            }
             return;
         }
         consume(0);
@@ -106,10 +120,20 @@ __global__ void __launch_bounds__(W * 64) stream_probe_kernel(const void* __rest
     }
 }
 
+// The output paia_probe_set_output installed (none by default).
+uint16_t* g_out_y = nullptr;
+uint32_t g_out_n = 0;
+
 template <int U, int W, bool LEAD = false>
 int launch_stream(const void* buf, uint32_t nbytes, uint32_t* sink, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((stream_probe_kernel<U, W, LEAD>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink);
+    if (g_out_n == 0) {
+        hipLaunchKernelGGL((stream_probe_kernel<U, W, LEAD, false>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink,
+                           nullptr, 0u);
+        return (int)hipGetLastError();
+    }
+    hipLaunchKernelGGL((stream_probe_kernel<U, W, LEAD, true>), dim3(grid), dim3(W * 64), 0, st, buf, nbytes, sink,
+                       g_out_y, g_out_n);
     return (int)hipGetLastError();
 }
 
@@ -135,12 +159,18 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     hipStream_t st = static_cast<hipStream_t>(stream);
     const u32x4* p = static_cast<const u32x4*>(buf);
     uint32_t* s = static_cast<uint32_t*>(sink);
+    uint16_t* y = g_out_y;
+    const uint32_t no = g_out_n;
+#define READ_CASE(UN)                                                                                              \
+    case UN:                                                                                                       \
+        if (no) hipLaunchKernelGGL((read_probe_kernel<UN, true>), dim3(grid), dim3(256), 0, st, p, n16, s, y, no); \
+        else hipLaunchKernelGGL((read_probe_kernel<UN, false>), dim3(grid), dim3(256), 0, st, p, n16, s, y, no);   \
+        break;
     switch (unroll) {
-    case 1: hipLaunchKernelGGL(read_probe_kernel<1>, dim3(grid), dim3(256), 0, st, p, n16, s); break;
-    case 4: hipLaunchKernelGGL(read_probe_kernel<4>, dim3(grid), dim3(256), 0, st, p, n16, s); break;
-    case 8: hipLaunchKernelGGL(read_probe_kernel<8>, dim3(grid), dim3(256), 0, st, p, n16, s); break;
+    READ_CASE(1) READ_CASE(4) READ_CASE(8)
     default: return -1;
     }
+#undef READ_CASE
     return (int)hipGetLastError();
 }
 
@@ -177,6 +207,15 @@ __attribute__((visibility("default"))) int paia_probe_stream_lead(const void* bu
     uint32_t* s = static_cast<uint32_t*>(sink);
     const uint32_t n = (uint32_t)nbytes;
     return U == 8 ? launch_stream<8, 8, true>(buf, n, s, grid, st) : launch_stream<16, 8, true>(buf, n, s, grid, st);
+}
+
+// y: nout bf16 values (nout < 2^31); nout = 0 (y ignored) turns the writes off.
+__attribute__((visibility("default"))) int paia_probe_set_output(void* y, size_t nout)
+{
+    if (nout >= (1ull << 31) || (nout && (!y || (reinterpret_cast<uintptr_t>(y) & 1)))) return -2;
+    g_out_y = nout ? static_cast<uint16_t*>(y) : nullptr;
+    g_out_n = (uint32_t)nout;
+    return 0;
 }
 
 __attribute__((visibility("default"))) int paia_probe_copy(const void* src, void* dst, size_t nbytes, int grid,

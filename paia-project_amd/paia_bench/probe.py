@@ -31,6 +31,8 @@ def load_probe():
     lib.paia_probe_stream_lead.restype = ctypes.c_int
     lib.paia_probe_stream_lead.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
                                            ctypes.c_int, ctypes.c_void_p]
+    lib.paia_probe_set_output.restype = ctypes.c_int
+    lib.paia_probe_set_output.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     lib.paia_probe_copy.restype = ctypes.c_int
     lib.paia_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
     lib.paia_probe_empty.restype = ctypes.c_int
@@ -120,10 +122,12 @@ def slice_plan(buf_bytes: int, S: int) -> tuple:
     return stride, n
 
 
-def b0_sized(P, buf, sink, cus, S: int, configs=SIZED_CONFIGS) -> dict:
+def b0_sized(P, buf, sink, cus, S: int, configs=SIZED_CONFIGS, y=None, nout: int = 0) -> dict:
     """The read floor for S bytes: reads of S bytes from distinct slices of `buf`, back to back in one graph (the
     GEMV timings' cold-cache rotation); a screen of every launch shape, then the best µs per read of the FINALISTS
-    timed as the GEMVs are."""
+    timed as the GEMVs are. With nout > 0 (y: a device tensor of at least nout bf16), also the I/O floor: reads of S
+    bytes that also write nout bf16 outputs, the best of the read finalists and the two best grid-stride shapes of the
+    screen (whose writes come at the very end), timed the same way (io_us, io_cfg)."""
     from paia_gemv.loader import current_raw_stream
 
     from .timing import capture, replay_ms, stats
@@ -136,8 +140,21 @@ def b0_sized(P, buf, sink, cus, S: int, configs=SIZED_CONFIGS) -> dict:
                              for j in range(R)], warm=1)
         screen.append((stats(replay_ms(g, 3))["median"] * 1e3 / R, cfg))
         del g
-    best = min((_final_us(P, cfg, S, slices, sink, cus), cfg) for _, cfg in sorted(screen)[:FINALISTS])
-    return {"bytes": S, "us": best[0], "gbps": S / (best[0] * 1e-6) / 1e9, "cfg": list(best[1])}
+    finalists = [cfg for _, cfg in sorted(screen)[:FINALISTS]]
+    best = min((_final_us(P, cfg, S, slices, sink, cus), cfg) for cfg in finalists)
+    out = {"bytes": S, "us": best[0], "gbps": S / (best[0] * 1e-6) / 1e9, "cfg": list(best[1])}
+    if nout > 0:
+        if y is None or y.numel() * y.element_size() < 2 * nout:
+            raise ValueError("the I/O floor needs an output buffer of nout bf16")
+        if P.paia_probe_set_output(y.data_ptr(), nout):
+            raise RuntimeError(f"probe output of {nout} values refused")
+        gs_best = [cfg for _, cfg in sorted(screen) if cfg[0] == "gs"][:2]
+        try:
+            io = min((_final_us(P, cfg, S, slices, sink, cus), cfg) for cfg in dict.fromkeys(finalists + gs_best))
+        finally:
+            P.paia_probe_set_output(None, 0)
+        out.update(io_us=io[0], io_cfg=list(io[1]), nout=nout)
+    return out
 
 
 def main(argv=None):

@@ -159,3 +159,15 @@ def test_every_probe_shape_is_instantiated():
     assert P.paia_probe_stream(None, 1 << 20, None, 16, 16, 256, None) == -1       # spills: not instantiated
     assert P.paia_probe_stream(None, 1 << 20, None, 4, 1, 256, None) == -1
     assert P.paia_probe_stream_lead(None, 1 << 20, None, 4, 256, None) == -1
+
+
+def test_probe_output_setting_is_checked():
+    """The I/O-floor output of the read probes: refused without a buffer, odd-aligned or >= 2^31 values; nout = 0
+    (the default) turns the writes off. No GPU work."""
+    from paia_bench.probe import load_probe
+    P = load_probe()
+    assert P.paia_probe_set_output(None, 4096) == -2
+    assert P.paia_probe_set_output(1, 4096) == -2                  # not 2-byte aligned
+    assert P.paia_probe_set_output(2, 1 << 31) == -2
+    assert P.paia_probe_set_output(2, 4096) == 0
+    assert P.paia_probe_set_output(None, 0) == 0
