@@ -10,7 +10,10 @@ the reference. Extra, beyond the reference's test:
   * BF16 and FP8 with all-zero weights must give exactly +0 in every row (every product is 0);
   * the INT4 kernels compute s * (sum (128+q) x - (128+z) sum x), a cancellation of two terms of size ~128 |sum x|:
     zero weights with |x| ~ 100 (x ~ 100 N(0,1)) must stay within the gate;
-  * the naive and unfused INT4 controls and the small-batch pick (M = 2, 4, 16) see the same operands.
+  * the naive and unfused INT4 controls and the small-batch pick (M = 2, 4, 16) see the same operands;
+  * activations over a wide range of magnitudes: "wide" (|x| = 2^-50 .. 2^50, random signs) and "bigx" (|x| up to
+    2^62): the INT4 kernels that stage x scale it by 2^64 in bf16 to read the nibbles as bf16 subnormals, and are
+    exact for |x| < 2^64 (products q|x| >= 2^-57); these operands sit inside that range at both ends.
 """
 import numpy as np
 import pytest
@@ -44,6 +47,11 @@ def special_operands(fmt, special, seed=5):
     elif special == "zeros_x100":       # zero weights, |x| ~ 100
         W = torch.zeros_like(W)
         x = torch.randn(K, generator=g) * 100.0
+    elif special in ("wide", "bigx"):   # |x| = m * 2^e, m in [1, 2), random signs
+        lo, hi = (-50, 50) if special == "wide" else (50, 61)
+        e = torch.randint(lo, hi + 1, (K,), generator=g).double()
+        sgn = torch.where(torch.rand(K, generator=g) < 0.5, -1.0, 1.0).double()
+        x = (sgn * (1.0 + torch.rand(K, generator=g).double()) * torch.pow(2.0, e)).float()
     else:
         raise ValueError(special)
     o = {"fmt": fmt, "N": N, "K": K, "x": x.to(torch.bfloat16), "bias": None}
@@ -80,7 +88,8 @@ def prepared(oracle, fmt, special, cuda):
     return o, np_ops, to_device(o, cuda)
 
 
-CASES = [(f, sp) for f in FORMATS for sp in ("zeros", "large")] + [("int4", "zeros_x100"), ("int4zp", "zeros_x100")]
+CASES = ([(f, sp) for f in FORMATS for sp in ("zeros", "large", "wide", "bigx")] +
+         [("int4", "zeros_x100"), ("int4zp", "zeros_x100")])
 
 
 @pytest.mark.parametrize("fmt,special", CASES)
