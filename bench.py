@@ -194,16 +194,16 @@ def cpu_baseline(lib, budget_s: float = 30.0) -> dict:
             "cpu": cpu_model(), "per_config": rows}
 
 
-def load_traffic(case_name: str):
+def load_traffic(case_name: str, kernel: str):
     """HBM bytes per launch of this GEMV case from the committed rocprofv3 PMC summary (profiles/pmc_traffic.json,
-    written by `python -m paia_bench.pmc summarize`), or None if that case was not profiled."""
+    written by `python -m paia_bench.pmc summarize`), or None if that case was not profiled with this kernel."""
     f = ROOT / "profiles" / "pmc_traffic.json"
     if not f.exists():
         return None
     try:
         d = json.loads(f.read_text())
         e = d.get("cases", {}).get(case_name)
-        return None if e is None else {"bytes": round(e["traffic_bytes"]), "kernel": e.get("kernel"),
+        return None if e is None or e.get("kernel") != kernel else {"bytes": round(e["traffic_bytes"]), "kernel": e.get("kernel"),
                                        "fetch_bytes": round(e["fetch_bytes"]), "write_bytes": round(e["write_bytes"]),
                                        "over_algorithmic": e.get("traffic_over_algorithmic")}
     except (OSError, ValueError, KeyError):
@@ -220,7 +220,7 @@ def kernel_name(lib, fmt, variant) -> str:
 
 
 def roofline_entry(lib, name, e):
-    traffic = load_traffic(name)
+    traffic = load_traffic(name, e["kernel"])
     return {"bound": "hbm", "achieved": e["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(e["gbps"] / PEAK_GBPS, 4), "traffic": traffic["bytes"] if traffic else None,
             "kernel": e["kernel"], "case": name, "avg_launch_us": e["us"], "algorithmic_bytes": e["bytes"],
