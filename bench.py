@@ -17,7 +17,7 @@ Printed: ONE JSON line (the driver's contract) with value = aggregate algorithmi
                 of R back-to-back launches rotating over >= 4 x 256 MiB of copies of that shape alone: configs[0]
                 BF16 o_proj, configs[1] the four FP8 Llama shapes, configs[2] the four INT4 (asymmetric g128) Llama
                 shapes, configs[3] the Qwen2.5-7B shapes in all three formats (qkv with its bias) and the bf16
-                lm_head, configs[4]'s bf16 Llama lm_head; each case on A (default 3) independent allocations,
+                lm_head, configs[4]'s bf16 Llama lm_head; each case on A (default 5) independent allocations,
                 each gated (copy 0 against the CPU reference) before it is timed, the median across them reported
   roofline      the dominant kernel of the workload (FP8 gate_up): algorithmic bytes / its average launch time
                 (hipEvents on the launch stream, inside this run) vs 8 TB/s; traffic = HBM bytes per launch from the
@@ -228,21 +228,23 @@ def roofline_entry(lib, name, e):
             "traffic_detail": traffic}
 
 
-def measure_per_gemv(lib, dev, allocations: int = 3) -> dict:
+def measure_per_gemv(lib, dev, allocations: int | None = None) -> dict:
     """Every GEMV of PER_GEMV on its own rotation (>= 4 x 256 MiB of copies of that shape), on `allocations`
-    independent allocations, each built, gated (copy 0, sampled rows) and freed in turn; the reported time is the
-    median across them (the reference harness's allocations per cell, paia-bench/configs/shapes.yaml:77,
-    paia-bench/bench/run.py:201-254: fresh allocations of one op differ by physical placement)."""
+    independent allocations (default 5, as the reference), each built, gated (copy 0, sampled rows), timed and
+    freed in turn, with R sized on the first and kept; the reported time is the median across them (the reference
+    harness's cell protocol, paia-bench/configs/shapes.yaml:72-80, paia-bench/bench/run.py:200-270: fresh
+    allocations of one op differ by physical placement)."""
     import torch
     from paia_bench.cases import GemvCase
     from paia_bench.chain import sample_rows
-    from paia_bench.timing import plan_rotation, time_per_call_us
+    from paia_bench.timing import ALLOCATIONS_PER_CELL, CELL_SAMPLE_TARGET_MS, plan_rotation, time_per_call_us
 
     per = {}
     for cfg, fmt, model, nm, N, K, bias in PER_GEMV:
         name = case_name(fmt, model, nm, N, K, bias)
-        us_a, worst = [], 0.0
-        for _ in range(max(1, allocations)):
+        us_a, n_a, worst, R = [], [], 0.0, None
+        k = max(1, ALLOCATIONS_PER_CELL if allocations is None else allocations)
+        for _ in range(k):
             c = GemvCase(lib, fmt, N, K, bias=bias, name=name)
             n_rot = plan_rotation(c.footprint())["n_copies"]
             c.build(n_rot, dev, host_copy0=False)
@@ -251,8 +253,10 @@ def measure_per_gemv(lib, dev, allocations: int = 3) -> dict:
             if not chk["ok"]:
                 raise RuntimeError(f"{name} failed the correctness gate: {chk}")
             worst = max(worst, chk["rel_err"])
-            t = time_per_call_us(c.call, n_rot)
+            t = time_per_call_us(c.call, n_rot, sample_target_ms=CELL_SAMPLE_TARGET_MS / k, R=R)
+            R = t["R"]
             us_a.append(t["us"])
+            n_a.append(t["us_n"])
             c.free()
             torch.cuda.empty_cache()
         us = statistics.median(us_a)
@@ -261,7 +265,8 @@ def measure_per_gemv(lib, dev, allocations: int = 3) -> dict:
         per[name] = {"config": cfg, "N": N, "K": K, "us": round(us, 3), "gbps": round(gbps, 1),
                      "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "variant": fam[c.variant],
                      "kernel": kernel_name(lib, fmt, c.variant), "bytes": c.bytes()["total"], "R": t["R"],
-                     "copies": n_rot, "us_allocations": [round(u, 3) for u in us_a], "rel_err": round(worst, 5)}
+                     "copies": n_rot, "us_allocations": [round(u, 3) for u in us_a], "samples_per_allocation": n_a,
+                     "alloc_spread_pct": round(100 * (max(us_a) - min(us_a)) / us, 3), "rel_err": round(worst, 5)}
         log(f"  {name}: {us:.2f} us  {gbps:.0f} GB/s  ({100 * gbps / PEAK_GBPS:.1f}% of 8 TB/s), "
             f"allocations {' '.join(f'{u:.2f}' for u in us_a)}")
     return per
@@ -277,8 +282,9 @@ def main(argv=None):
     ap.add_argument("--no-b0", action="store_true", help="skip the streaming-read probe (B0) leg")
     ap.add_argument("--no-chain", action="store_true", help="skip the decode-chain (configs[4]) measurement")
     ap.add_argument("--no-per-gemv", action="store_true", help="skip the per-GEMV figures (and b0, roofline)")
-    ap.add_argument("--allocations", type=int, default=3,
-                    help="independent operand allocations per per-GEMV case; the median across them is reported")
+    ap.add_argument("--allocations", type=int, default=None,
+                    help="independent operand allocations per per-GEMV case (default 5); the median across them is "
+                         "reported")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}). The M=1 GEMV shards along N "

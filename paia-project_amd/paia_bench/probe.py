@@ -70,8 +70,9 @@ def probe_launch(P, cfg, ptr, nbytes, sink_ptr, cus, stream):
 
 
 # The screen of every launch shape times a few replays straight after capture; the FINALISTS best shapes are then
-# timed the way the GEMVs are (paia_bench.timing.time_per_call_us: the same rotation, 100 ms of warm-up replays,
-# median of 30), so a floor and a GEMV time come from the same clock state and the same statistic.
+# timed the way one allocation of a GEMV is (paia_bench.timing.time_per_call_us: the same rotation, >= 200 ms and 20
+# calls of warm-up, then 200 ms of samples, 30 at least; the median), so a floor and a GEMV time come from the same
+# clock state and the same statistic.
 FINALISTS = 3
 
 

@@ -64,24 +64,47 @@ def stats(samples: list) -> dict:
             "cv": (statistics.pstdev(s) / mean) if n > 1 and mean > 0 else 0.0, "n": n}
 
 
-def time_per_call_us(call, n_copies: int, target_ms: float = 5.0, samples: int = 30, warmup_ms: float = 100.0,
+# The reference harness's cell protocol (paia-bench/configs/shapes.yaml:72-80, paia-bench/bench/timing.py:111-172,
+# paia-bench/bench/run.py:200-270): per allocation a warm-up of >= 20 calls and >= 200 ms, then
+# clamp(sample_target / unit, 30, 300) timed units, where a cell's 1000 ms sample target is split over its 5
+# allocations; R is sized on the first allocation and kept for the others; the cell's value is the median across
+# allocations.
+WARMUP_MIN_CALLS = 20
+WARMUP_MIN_MS = 200.0
+SAMPLES_MIN, SAMPLES_MAX = 30, 300
+CELL_SAMPLE_TARGET_MS = 1000.0
+ALLOCATIONS_PER_CELL = 5
+
+
+def time_per_call_us(call, n_copies: int, target_ms: float = 5.0, samples: int | None = None,
+                     warmup_ms: float = WARMUP_MIN_MS, warmup_calls: int = WARMUP_MIN_CALLS,
+                     sample_target_ms: float = CELL_SAMPLE_TARGET_MS / ALLOCATIONS_PER_CELL, R: int | None = None,
                      r_max: int = 4000) -> dict:
     """Per-call microseconds of call(i) (launch on copy i): one graph of R back-to-back calls cycling the copies,
-    R sized so a replay lasts >= target_ms; median over `samples` replays."""
-    # estimate from a short graph
-    r0 = min(r_max, max(8, 2 * n_copies))
-    g = capture(lambda: [call(j % n_copies) for j in range(r0)])
-    est = statistics.median(replay_ms(g, 3)) * 1e3 / r0
-    del g
-    R = int(min(r_max, max(r0, math.ceil(target_ms * 1e3 / max(est, 1e-3)))))
+    R sized so a replay lasts >= target_ms (or the R given, e.g. the first allocation's, rounded to whole rotations);
+    warm-up replays until both warmup_calls calls and warmup_ms have passed; then `samples` timed replays, or, when
+    samples is None, clamp(sample_target_ms / replay time, 30, 300) of them; the median per call."""
+    if R is None:
+        # estimate from a short graph
+        r0 = min(r_max, max(8, 2 * n_copies))
+        g = capture(lambda: [call(j % n_copies) for j in range(r0)])
+        est = statistics.median(replay_ms(g, 3)) * 1e3 / r0
+        del g
+        R = int(min(r_max, max(r0, math.ceil(target_ms * 1e3 / max(est, 1e-3)))))
     R = max(n_copies, (R // n_copies) * n_copies)                # whole rotations
     g = capture(lambda: [call(j % n_copies) for j in range(R)])
-    t0 = time.perf_counter()
-    while (time.perf_counter() - t0) * 1e3 < warmup_ms:
+    t0, calls = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < warmup_ms or calls < warmup_calls:
         g.replay()
+        calls += R
     torch.cuda.synchronize()
+    w_ms = (time.perf_counter() - t0) * 1e3
+    if samples is None:
+        unit_ms = statistics.median(replay_ms(g, 3))
+        samples = int(min(SAMPLES_MAX, max(SAMPLES_MIN, math.ceil(sample_target_ms / max(unit_ms, 1e-3)))))
     ms = replay_ms(g, samples)
     del g
     per = [m * 1e3 / R for m in ms]
     st = stats(per)
-    return {"us": st["median"], "R": R, "n_copies": n_copies, **{f"us_{k}": v for k, v in st.items() if k != "median"}}
+    return {"us": st["median"], "R": R, "n_copies": n_copies, "warmup_calls": calls, "warmup_ms": round(w_ms, 1),
+            **{f"us_{k}": v for k, v in st.items() if k != "median"}}
