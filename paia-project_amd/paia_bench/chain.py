@@ -8,8 +8,9 @@ distributions on the device from a generator seeded 1000 + N + K + 7919. The who
 streams from HBM on every replay; the 256 MiB Infinity Cache holds none of it across a replay.
 
 The launches are serialised exactly as in a decode step, in its order (layer by layer: qkv, o, gate_up, down; one
-stream, each GEMV starts when the previous one has finished). The GEMV inputs x are fixed per launch: this chain measures the linear layers only; attention, norms and
-activations that would sit between them are not part of the path.
+stream, each GEMV starts when the previous one has finished). The GEMV inputs x are fixed per launch: this chain
+measures the linear layers only; attention, norms and activations that would sit between them are not part of the
+path.
 """
 from __future__ import annotations
 
