@@ -122,12 +122,13 @@ PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
  * alignment and the K rules are those of the M = 1 entry point of the same format. bias bf16 [N] or NULL.
  * kind: 0 BF16, 1 FP8, 2 INT4 reference format, 3 INT4 asymmetric. variant < 0 = paia_gemv_batch_pick_variant's.
  * Knobs: P tiles of 16 rows per wave, U k-blocks of 128 columns in flight per wave, W waves per block, S waves
- * sharing a tile along K, X = 0 x staged in LDS per K-chunk / 1 x loaded with the weights. P = 0 marks a
+ * sharing a tile along K, X = 0 x staged in LDS per K-chunk of up to 64 KiB / 1 x loaded with the weights / 2 x
+ * staged as for 0 in K-chunks of up to 80 KiB (or the device's per-block LDS if less). P = 0 marks a
  * row-streaming variant (the M = 1 kernel's weight stream with one accumulator per activation row): U 1-KiB chunks
  * per item, W waves per block, S weight rows per wave, and X the one M (2-6; BF16 and FP8 2-8) it serves. The last variant of
  * each table (P = U = W = S = 0, X = 1) is the M = 1 GEMV itself with paia_gemv_pick_variant's choice (M = 1 only;
- * the batch alignment rules hold for it, y included). Returns 0, -1 bad variant, -2 bad shape/alignment (or, X = 0,
- * S*M*U too large for the LDS chunk; or, P = 0, another M or M copies of the staged x beyond the device's per-block
+ * the batch alignment rules hold for it, y included). Returns 0, -1 bad variant, -2 bad shape/alignment (or, X = 0
+ * or 2, S*M*U too large for the LDS chunk; or, P = 0, another M or M copies of the staged x beyond the device's per-block
  * LDS, 160 KiB on MI355X), > 0
  * hipError_t. */
 PAIA_API int paia_gemv_batch_variant_count(int kind);

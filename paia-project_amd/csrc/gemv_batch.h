@@ -419,13 +419,17 @@ __global__ void __launch_bounds__(W * kWave) gemv_batch_kernel(BatchParams p)
 // host side
 // ---------------------------------------------------------------------------------------------------------------
 
-// LDS a batch launch may use (bytes).
+// LDS a batch launch may use (bytes): the default budget, and the wider one of the X = 2 variants (x staged as for
+// X = 0 in chunks of up to 80 KiB: two blocks still fit a 160 KiB CU, and fewer chunks mean fewer x reloads and
+// barriers at M = 8..16).
 constexpr uint32_t kBatchLds = 65536;
+constexpr uint32_t kBatchLdsWide = 81920;
 
-// Fill in the launch plan (k-blocks, splits, chunking, LDS). Returns the LDS bytes (possibly 0 for X=1 without
-// split-K), or -1 if no chunk of U k-blocks fits (X=0: too many activation rows x splits for this U).
+// Fill in the launch plan (k-blocks, splits, chunking, LDS) within `budget` bytes of LDS. Returns the LDS bytes
+// (possibly 0 for X=1 without split-K), or -1 if no chunk of U k-blocks fits (X=0: too many activation rows x splits
+// for this U).
 template <int P, int U, int W, int XM, int MG>
-int64_t batch_plan(BatchParams& p)
+int64_t batch_plan(BatchParams& p, uint32_t budget)
 {
     p.KB = (p.K + kBlockCols - 1) / kBlockCols;
     p.ntiles = (p.N + kTileRows - 1) / kTileRows;
@@ -441,8 +445,8 @@ int64_t batch_plan(BatchParams& p)
     }
     const uint32_t per_kb = batch_x_bytes(p.S, p.M, 1) - batch_x_bytes(p.S, p.M, 0);
     const uint32_t fixed = batch_x_bytes(p.S, p.M, 0);
-    if (fixed + per_kb * U > kBatchLds) return -1;
-    int C = (int)((kBatchLds - fixed) / per_kb);
+    if (fixed + per_kb * U > budget) return -1;
+    int C = (int)((budget - fixed) / per_kb);
     C -= C % U;
     if (C > cap) C = cap;
     p.C = C;
@@ -452,12 +456,23 @@ int64_t batch_plan(BatchParams& p)
     return xb > pb ? xb : pb;
 }
 
-// Launch on `st`. Arguments were validated by the caller (1 <= M <= 16, S divides W). Returns 0, -2 or a hipError_t.
+// Launch on `st` with at most `budget` bytes of LDS. Arguments were validated by the caller (1 <= M <= 16, S divides
+// W). Returns 0, -2 or a hipError_t.
 template <int F, int P, int U, int W, int XM, int MG>
-int launch_batch_mg(BatchParams p, hipStream_t st)
+int launch_batch_mg(BatchParams p, hipStream_t st, uint32_t budget)
 {
-    const int64_t lds = batch_plan<P, U, W, XM, MG>(p);
+    const int64_t lds = batch_plan<P, U, W, XM, MG>(p, budget);
     if (lds < 0) return -2;
+    if (lds > (int64_t)kBatchLds) {   // beyond the default dynamic-LDS limit: raise it once for this kernel
+        static std::atomic<int> raised{0};
+        if (!raised.load(std::memory_order_relaxed)) {
+            const hipError_t e =
+                hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_batch_kernel<F, P, U, W, XM, MG>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)budget);
+            if (e != hipSuccess) return (int)e;
+            raised.store(1, std::memory_order_relaxed);
+        }
+    }
     const int tiles_per_block = (W / p.S) * P;
     const int grid = (p.ntiles + tiles_per_block - 1) / tiles_per_block;
     hipLaunchKernelGGL((gemv_batch_kernel<F, P, U, W, XM, MG>), dim3(grid), dim3(W * kWave), (uint32_t)lds, st, p);
@@ -466,12 +481,12 @@ int launch_batch_mg(BatchParams p, hipStream_t st)
 
 // INT4 with stages in fours and G % 4 == 0 (every Llama / Qwen shape) takes the grouped-metadata kernel.
 template <int F, int P, int U, int W, int XM>
-int launch_batch(BatchParams p, hipStream_t st)
+int launch_batch(BatchParams p, hipStream_t st, uint32_t budget = kBatchLds)
 {
     if constexpr ((F == kI4 || F == kI4ZP) && U % 4 == 0) {
-        if ((p.K / kBlockCols) % 4 == 0) return launch_batch_mg<F, P, U, W, XM, 4>(p, st);
+        if ((p.K / kBlockCols) % 4 == 0) return launch_batch_mg<F, P, U, W, XM, 4>(p, st, budget);
     }
-    return launch_batch_mg<F, P, U, W, XM, 1>(p, st);
+    return launch_batch_mg<F, P, U, W, XM, 1>(p, st, budget);
 }
 
 using BatchLaunchFn = int (*)(BatchParams, hipStream_t);

@@ -9,7 +9,8 @@
 //
 // Variant knobs: P tiles of 16 rows per wave, U k-blocks (128 columns) of loads in flight per wave, W waves per block,
 // S waves sharing a tile along K (split-K inside the block), X how x reaches the matrix cores (0 staged in LDS per
-// K-chunk, 1 loaded with the weights). variant < 0 selects paia_gemv_batch_pick_variant's.
+// K-chunk of up to 64 KiB, 1 loaded with the weights, 2 staged as for 0 in chunks of up to 80 KiB, or the device's
+// per-block LDS if less). variant < 0 selects paia_gemv_batch_pick_variant's.
 //
 // P = 0 marks the row-streaming kernel instead (gemv_rows_kernel: the M = 1 GEMV's weight stream and decode with one
 // accumulator per activation row, for M = 2..6, BF16 and FP8 also 7, 8): then U is its 1-KiB chunks per item, W its waves per
@@ -27,9 +28,13 @@
 namespace {
 using namespace paia;
 
+// LDS budget of the X = 2 variants on this device
+uint32_t wide_lds() { return rows_max_lds() < kBatchLdsWide ? rows_max_lds() : kBatchLdsWide; }
+
 template <int F, int P, int U, int W, int X>
 int launch_b(BatchParams p, hipStream_t st)
 {
+    if constexpr (X == 2) return launch_batch<F, P, U, W, 0>(p, st, wide_lds());
     return launch_batch<F, P, U, W, X>(p, st);
 }
 
@@ -87,7 +92,7 @@ int launch_m1_b(BatchParams b, hipStream_t st)
                    RV_M8(F, 2, 1, 16)
 #define BV_S(F, P, U, X) BV(F, P, U, 4, 1, X) BV(F, P, U, 4, 2, X) BV(F, P, U, 4, 4, X) \
                          BV(F, P, U, 8, 1, X) BV(F, P, U, 8, 2, X) BV(F, P, U, 8, 4, X) BV(F, P, U, 8, 8, X)
-#define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1)
+#define BV_W(F, P, U) BV_S(F, P, U, 0) BV_S(F, P, U, 1) BV_S(F, P, U, 2)
 // register budget: P * U * (16-byte loads per k-block) <= 16 buffers of 4 VGPRs (INT4 P=2 U=8 with x loaded
 // alongside spilled, so it is left out)
 const BatchVariant kBf16Batch[] = {BV_W(kBF16, 1, 2) BV_W(kBF16, 1, 4) BV_W(kBF16, 2, 2) RV_ALL(kBF16)
@@ -138,7 +143,7 @@ int find(const Table& t, int P, int U, int W, int S, int X)
 bool fits(const BatchVariant& v, int M)
 {
     if (v.P == 0) return v.X == M;
-    return v.X == 1 || batch_x_bytes(v.S, M, v.U) <= kBatchLds;
+    return v.X == 1 || batch_x_bytes(v.S, M, v.U) <= (v.X == 2 ? wide_lds() : kBatchLds);
 }
 
 // Default choice: a measured entry for the shape and M when the tuned table has one; otherwise a rule fitted to MI355X

@@ -24,6 +24,7 @@ from oracle import oracle as O
 from test_decode_emulation import C43, i4_decode_pairs
 
 LDS = 65536
+LDS_WIDE = 81920        # the X = 2 variants' budget (gemv_batch.h kBatchLdsWide), capped by the device's limit
 KINDS = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}
 
 
@@ -138,8 +139,10 @@ def test_int4_decode_constant_is_bf16_128():
 # ---------------------------------------------------------------------------------------------------------------
 # work decomposition
 # ---------------------------------------------------------------------------------------------------------------
-def plan(fmt, M, N, K, P, U, W, S, X=0):
-    """gemv_batch.h batch_plan + launch_batch (None when, X=0, no chunk of U k-blocks fits)."""
+def plan(fmt, M, N, K, P, U, W, S, X=0, lds_limit=LDS_WIDE):
+    """gemv_batch.h batch_plan + launch_batch (None when, X=0 or 2, no chunk of U k-blocks fits). X = 2 stages x as
+    X = 0 within min(LDS_WIDE, lds_limit) bytes (the library's wide_lds(); lds_limit: the device's per-block LDS, at
+    least 64 KiB)."""
     KB = -(-K // 128)
     kbs = -(-KB // S)
     mg = 4 if fmt in ("int4", "int4zp") and U % 4 == 0 and KB % 4 == 0 else 1
@@ -151,11 +154,12 @@ def plan(fmt, M, N, K, P, U, W, S, X=0):
     common = dict(KB=KB, kbs=kbs, ntiles=ntiles, grid=-(-ntiles // ((W // S) * P)))
     if X == 1:
         return dict(common, C=cap, nchunks=1, xrow=0, x_end=0, lds=pb, mg=mg)
+    budget = LDS if X == 0 else min(LDS_WIDE, max(LDS, lds_limit))
     per_kb = S * M * 256
     fixed = S * M * 16
-    if fixed + per_kb * U > LDS:
+    if fixed + per_kb * U > budget:
         return None
-    C = min((LDS - fixed) // per_kb // U * U, cap)
+    C = min((budget - fixed) // per_kb // U * U, cap)
     xrow = C * 256 + 16
     return dict(common, C=C, nchunks=-(-kbs // C), xrow=xrow, x_end=S * M * xrow, lds=max(S * M * xrow, pb), mg=mg)
 
@@ -163,10 +167,11 @@ def plan(fmt, M, N, K, P, U, W, S, X=0):
 def replay(fmt, M, N, K, P, U, W, S, X=0):
     p = plan(fmt, M, N, K, P, U, W, S, X)
     assert p is not None
+    assert p["lds"] <= (LDS_WIDE if X == 2 else LDS)
     seen = np.zeros((p["ntiles"], p["KB"]), dtype=np.int64)
     C, kbs = p["C"], p["kbs"]
     assert C % U == 0 and C >= U
-    if X == 0:
+    if X != 1:
         # staging: vector q of chunk c -> (split, row, kbl, v); LDS addresses inside the x region
         nvec = S * M * C * 16
         assert (nvec - 1) // 16 // C // M < S
@@ -192,7 +197,7 @@ def replay(fmt, M, N, K, P, U, W, S, X=0):
                             # the chunk slot read holds k-block split*kbs + c*C + kbl of this split
                             assert split * kbs + c * C + kbl == kb and kb < p["KB"]
                             # A-fragment reads stay in the split's rows of this chunk
-                            if X == 0:
+                            if X != 1:
                                 assert (split * M + M - 1) * p["xrow"] + kbl * 256 + 256 <= p["x_end"]
                             for tt in range(P):
                                 if tile0 + tt < p["ntiles"]:
@@ -248,7 +253,7 @@ def runs(fmt, M, N, K, v, lds_limit=65536):
         return M == 1 and rows_lds(fmt, 1, K) + 512 <= 65536
     if v["P"] == 0:
         return v["X"] == M and rows_lds(fmt, M, K) <= lds_limit
-    return plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"]) is not None
+    return plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"], lds_limit) is not None
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4"])
@@ -257,7 +262,7 @@ def test_every_tile_and_k_block_once(fmt):
     shapes = [(1, 16 * 1 + 3, 128), (3, 100, 3 * 128), (2, 257, 1000 // kmult * kmult), (16, 64, 4096),
               (16, 40, 14336), (7, 4608, 3584), (5, 33, 18944)]
     n = 0
-    for (M, N, K), (P, U), (W, S), X in itertools.product(shapes, TABLE[fmt], WS, (0, 1)):
+    for (M, N, K), (P, U), (W, S), X in itertools.product(shapes, TABLE[fmt], WS, (0, 1, 2)):
         if K % kmult or plan(fmt, M, N, K, P, U, W, S, X) is None:
             continue
         replay(fmt, M, N, K, P, U, W, S, X)
@@ -271,7 +276,7 @@ def test_table_matches_library(gemv_lib):
     lim = rows_lds_limit()
     for fmt, k in KINDS.items():
         got = {(v["P"], v["U"], v["W"], v["S"], v["X"]) for v in L.variants_batch[fmt]}
-        want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1))}
+        want = {(P, U, W, S, X) for (P, U), (W, S), X in itertools.product(TABLE[fmt], WS, (0, 1, 2))}
         want |= {(0, U, W, R, M) for (R, U, W), M in itertools.product(ROWS, ROWS_M8 if fmt in ("bf16", "fp8") else ROWS_M6)}
         want.add((0, 0, 0, 0, 1))                       # the M = 1 GEMV entry, last in each table
         assert L.variants_batch[fmt][-1]["U"] == 0
