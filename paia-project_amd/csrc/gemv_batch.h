@@ -17,9 +17,10 @@
 //     (128 + z) * sum_k x[m,k] is removed per group, with the group sums of x taken by one more MFMA chain against a
 //     B operand of ones (it lands in the lanes and rows of D that need it, shared by the wave's P tiles).
 //   * x (the A operand) comes one of two ways (knob X):
-//       X=0: staged in LDS per K-chunk (all of K when M*K fits, as at M = 1) in the column order the format's MFMA
-//            steps take (INT4: (k, k+2, k+4, k+6, k+1, k+3, k+5, k+7) within each 8, matching the nibble decode);
-//            a chunk change costs two block barriers and drains the load pipeline.
+//       X=0: staged in LDS per K-chunk of up to 64 KiB (all of K when M*K fits, as at M = 1) in the column order the
+//            format's MFMA steps take (INT4: (k, k+2, k+4, k+6, k+1, k+3, k+5, k+7) within each 8, matching the
+//            nibble decode); a chunk change costs two block barriers and drains the load pipeline. X=2 is the same
+//            kernel with chunks of up to 80 KiB (fewer chunk changes; the launch raises the LDS limit).
 //       X=1: loaded per k-block straight into registers with the weights (L2-resident: x is at most 16 rows), in the
 //            same pipeline; no LDS, no barrier, no K limit -- the choice for many rows or long K.
 //   * Each wave owns P tiles and one of S K-splits; the S waves sharing a tile combine their fp32 partials through
