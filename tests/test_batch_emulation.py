@@ -298,5 +298,7 @@ def test_table_matches_library(gemv_lib):
                     rows = 2 <= M <= (8 if fmt == "bf16" else 4) and rows_lds(fmt, M, K) <= lim
                     rows = rows and not (fmt.startswith("int4") and M >= 4 and N >= 16384)
                     assert (d["P"] == 0) == rows, (fmt, M, N, K, d)
+                    if d["P"] >= 1 and d["X"] == 1 and M >= 8:   # x with the weights: four waves, <= 4 splits
+                        assert d["W"] == 4 and d["S"] <= 4, (fmt, M, N, K, d)
         assert L.batch_pick_variant(fmt, 17, 4096, 4096) == -1
         assert L.batch_pick_variant(fmt, 0, 4096, 4096) == -1
