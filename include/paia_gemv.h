@@ -16,9 +16,10 @@
  *   K <= 32256, FP8 K <= 31744); beyond that the call runs an x-from-global kernel (x read with each item's weights,
  *   split-K over 8 waves) whatever the variant, slower but with the same contract. All Llama-3.1-8B / Qwen2.5-7B
  *   shapes stage x.
- * INT4 x range: the M=1 INT4 kernels that stage x read the nibbles as bf16 subnormals against x scaled by 2^64, so an
- *   |x| >= 2^64 becomes inf there and a product q*|x| below 2^-57 loses bits (the reference has neither limit; the
- *   x-from-global kernel and the small-batch entry points are not affected).
+ * INT4 x range: the INT4 kernels that stage x on the M=1 design (the M=1 entry points, and the small-batch
+ *   row-streaming variants, P = 0) read the nibbles as bf16 subnormals against x scaled by 2^64, so an |x| >= 2^64
+ *   becomes inf there and a product q*|x| below 2^-57 loses bits (the reference has neither limit; the x-from-global
+ *   kernel and the small-batch matrix-core variants, P >= 1, are not affected).
  */
 #ifndef PAIA_GEMV_H
 #define PAIA_GEMV_H
