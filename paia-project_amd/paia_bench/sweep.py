@@ -175,9 +175,9 @@ def main(argv=None):
                   f"({100 * b['gbps'] / HBM_PEAK_GBPS:.1f}% of 8 TB/s)", flush=True)
         case.free()
         torch.cuda.empty_cache()
-    if a.out:
-        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
-        Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
+        if a.out:   # rewritten after every cell, so a run stopped early keeps the cells it finished
+            Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+            Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
     if a.write_tuned:
         write_tuned(Path(a.write_tuned), a.fmt, results)
     return 0
