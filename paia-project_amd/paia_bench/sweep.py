@@ -178,6 +178,9 @@ def main(argv=None):
         if a.out:   # rewritten after every cell, so a run stopped early keeps the cells it finished
             Path(a.out).parent.mkdir(parents=True, exist_ok=True)
             Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
+    if a.out:
+        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.out).write_text(json.dumps({"fmt": a.fmt, "results": results}, indent=1))
     if a.write_tuned:
         write_tuned(Path(a.write_tuned), a.fmt, results)
     return 0
