@@ -185,3 +185,77 @@ def test_traffic_entries_match_their_kernel(gemv_lib):
         assert bench.load_traffic(name, e["kernel"] + "x") is None
         f, N, K = shapes[name]
         assert e["kernel"] == bench.kernel_name(gemv_lib, f, gemv_lib.pick_variant(f, N, K)), name
+
+
+def _full_record_fixture():
+    """A full bench record of the shape main() builds (every BASELINE GEMV, B0 read floors, both chains, every CPU
+    row), with values of the size a real run prints."""
+    import bench
+    per, floors, cpu_rows = {}, {}, []
+    for cfg, f, m, nm, N, K, b in bench.PER_GEMV:
+        name = bench.case_name(f, m, nm, N, K, b)
+        per[name] = {"config": cfg, "N": N, "K": K, "us": 152.365, "gbps": 7156.3, "pct_of_8TBps": 89.5,
+                     "variant": {"id": 63, "R": 2, "U": 8, "W": 8, "S": 1, "H": 1},
+                     "kernel": "paia::gemv_kernel<0, 2, 8, 8, 2, true>", "bytes": 1090306048, "R": 32, "copies": 2,
+                     "us_allocations": [152.361, 153.087, 153.223, 152.1, 152.9],
+                     "samples_per_allocation": [44, 44, 44, 44, 44], "alloc_spread_pct": 0.415, "rel_err": 0.00211,
+                     "traffic_over_algorithmic": 1.0045, "pct_of_b0": 96.4, "over_read_floor": 1.037,
+                     "over_io_floor": 1.032}
+        floors[name] = {"bytes": 1090306048, "us": 147.973, "gbps": 7368.2, "cfg": ["lw", 16, 2], "io_us": 148.661,
+                        "io_cfg": ["lw", 16, 2], "nout": N}
+        cpu_rows.append({"config": cfg, "gemv": name, "bytes": 1090306048, "us_dequant_matmul": 123456.7,
+                         "us_matmul": 23456.7, "gbps_dequant_matmul": 1.555, "gbps_matmul": 4.321})
+    roof = {"bound": "hbm", "achieved": 6270.3, "peak": 8000.0, "unit": "GB/s", "frac": 0.7838,
+            "traffic": 118144334, "kernel": "paia::gemv_kernel<1, 2, 2, 4, 2, false>",
+            "case": "fp8_llama_gate_up_28672x4096", "avg_launch_us": 18.759, "algorithmic_bytes": 117620736,
+            "traffic_detail": {"bytes": 118144334, "kernel": "paia::gemv_kernel<1, 2, 2, 4, 2, false>",
+                               "fetch_bytes": 117919054, "write_bytes": 225280, "over_algorithmic": 1.0045}}
+    chain = {f: {"format": f, "model": "llama31_8b", "bytes_per_step": 8040221184, "gbps": 5473.2,
+                 "pct_of_8TBps": 68.4, "us_per_token_step": 1469.21, "us_p5": 1468.1, "us_p95": 1471.9,
+                 "replays": 20, "launches": 129, "max_rel_err": 0.0021,
+                 "replayed_outputs_checked": [f"x@{i}" for i in range(13)], "replayed_max_rel_err": 0.0021}
+             for f in ("int4zp", "fp8")}
+    cpu = {"value": 1.624, "unit": "GB/s", "cores": 16, "kind": "port",
+           "sample": "23 BASELINE GEMVs once per run (configs[0]-[4]: FP8, INT4-asym, BF16 at the Llama and Qwen "
+                     "shapes, lm_heads), seeded copy-0 operands; torch dequant + fp32 matmul, 16 threads, median of "
+                     "5 after 2 warm-ups; value = FP8 layer step (configs[1])",
+           "cpu": "AMD EPYC 9575F 64-Core Processor", "us_fp8_layer_step": 134567.8,
+           "us_fp8_layer_step_matmul_only": 23456.7, "gbps_fp8_layer_step_matmul_only": 9.3,
+           "per_config": cpu_rows, "skipped": [], "wall_s": 41.2}
+    return {"metric": bench.METRIC, "value": 5305.2, "unit": "GB/s", "n_gpus": 1, "steps": 200, "warmup": 20,
+            "ms_per_step": 0.041171, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8e4m3 weights x bf16 activations, fp32 accumulate",
+            "data": "synthetic (seeded N(0,0.02) weights quantised to e4m3fn; N(0,1) bf16 x)",
+            "config": {"workload": "FP8 W8A16 GEMV, M=1, Llama-3.1-8B layer: qkv 6144x4096, o 4096x4096, "
+                                   "gate_up 28672x4096, down 4096x14336 (BASELINE configs[1])",
+                       "layer_copies": 5, "rotation_bytes": 1091927040, "step_bytes": 218385408,
+                       "us_per_layer_step": 41.171, "pct_of_8TBps": 66.3, "timed_graph_primed": True},
+            "roofline": roof, "roofline_by_dtype": {"bf16": roof, "fp8": roof, "int4zp": roof}, "per_gemv": per,
+            "b0": {"gbps": 7389.1, "pct_of_8TBps": 92.4, "bytes": 2146435072, "cfg": ["lw", 16, 2],
+                   "read_floor": floors},
+            "chain": chain, "cpu_baseline": cpu, "device": "AMD Instinct MI355X", "cus": 256,
+            "timed_wall_ms": 8.3}
+
+
+def test_bench_line_is_compact():
+    """The one JSON line the driver parses stays under 4 KB with every field a full run fills (the round whose line
+    was 21.5 KB arrived truncated and unparsed), carries the contract keys, the dominant kernel's roofline with its
+    traffic, one roofline per format, every per-GEMV case and the CPU baseline summary."""
+    import bench
+    full = _full_record_fixture()
+    line = json.dumps(bench.compact_line(full, "gpurun_out/bench_report.json"))
+    assert len(line) < 4096, len(line)
+    out = json.loads(line)
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+              "vs_baseline", "dtype", "data", "config"):
+        assert out[k] == full[k], k
+    assert out["roofline"]["traffic"] == 118144334 and out["roofline"]["frac"] == 0.7838
+    assert set(out["roofline_by_dtype"]) == {"bf16", "fp8", "int4zp"}
+    assert set(out["per_gemv"]) == set(full["per_gemv"]) and len(out["per_gemv"]) == len(bench.PER_GEMV)
+    assert out["per_gemv"]["fp8_llama_o_4096x4096"] == [152.365, 89.5, 1.032]
+    cpu = out["cpu_baseline"]
+    assert cpu["cores"] == 16 and cpu["kind"] == "port" and cpu["gemvs_timed"] == len(bench.PER_GEMV)
+    assert out["chain"]["fp8"] == [1469.21, 5473.2, 68.4]
+    # a run with the optional legs skipped still forms the line
+    bare = dict(full, roofline=None, roofline_by_dtype={}, per_gemv={}, b0=None, chain=None, cpu_baseline=None)
+    assert json.loads(json.dumps(bench.compact_line(bare)))["per_gemv"] == {}
