@@ -229,13 +229,17 @@ def load_traffic(case_name: str, kernel: str):
         return None
 
 
-def kernel_name(lib, fmt, variant) -> str:
-    """The template instance of gemv_kernel a case launches (as rocprofv3 names it)."""
+def kernel_name(lib, fmt, variant, N, K) -> str:
+    """The template instance a case launches (as rocprofv3 names it): gemv_kernel, or gemv_kernel43 for INT4 launches
+    with few weight loads per wave, with the variant's knobs; gemv_kernel_xg (its fixed knobs) for K beyond the LDS."""
     fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
     v = fam[variant]
     F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[fmt]
     aux = (2 if v["S"] else 0) if fmt == "bf16" else 2
-    return f"paia::gemv_kernel<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
+    k = lib.launch_kind(fmt, N, K, variant)
+    if k == "gemv_kernel_xg":
+        return f"paia::gemv_kernel_xg<{F}, 1, 2, 8, {aux}, true>"
+    return f"paia::{k}<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
 
 
 def roofline_entry(lib, name, e):
@@ -282,7 +286,7 @@ def measure_per_gemv(lib, dev, allocations: int | None = None) -> dict:
         fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
         per[name] = {"config": cfg, "N": N, "K": K, "us": round(us, 3), "gbps": round(gbps, 1),
                      "pct_of_8TBps": round(100 * gbps / PEAK_GBPS, 1), "variant": fam[c.variant],
-                     "kernel": kernel_name(lib, fmt, c.variant), "bytes": c.bytes()["total"], "R": t["R"],
+                     "kernel": kernel_name(lib, fmt, c.variant, N, K), "bytes": c.bytes()["total"], "R": t["R"],
                      "copies": n_rot, "us_allocations": [round(u, 3) for u in us_a], "samples_per_allocation": n_a,
                      "alloc_spread_pct": round(100 * (max(us_a) - min(us_a)) / us, 3), "rel_err": round(worst, 5)}
         tr = load_traffic(name, per[name]["kernel"])

@@ -16,10 +16,10 @@
  *   K <= 32256, FP8 K <= 31744); beyond that the call runs an x-from-global kernel (x read with each item's weights,
  *   split-K over 8 waves) whatever the variant, slower but with the same contract. All Llama-3.1-8B / Qwen2.5-7B
  *   shapes stage x.
- * INT4 x range: the INT4 kernels that stage x on the M=1 design (the M=1 entry points, and the small-batch
- *   row-streaming variants, P = 0) read the nibbles as bf16 subnormals against x scaled by 2^64, so an |x| >= 2^64
- *   becomes inf there and a product q*|x| below 2^-57 loses bits (the reference has neither limit; the x-from-global
- *   kernel and the small-batch matrix-core variants, P >= 1, are not affected).
+ * INT4 x: any finite bf16 activations, as in the reference. The M=1 kernels that stage x read the nibbles either
+ *   as bf16 subnormals against x scaled by a power of two (2^64 when the row's largest |x| lies in [2^-20, 2^64),
+ *   else a power picked from that largest |x|, so every staged value and product stays a normal number) or, on
+ *   launches with few weight loads per wave, as bf16 (128 + q) against unscaled x.
  */
 #ifndef PAIA_GEMV_H
 #define PAIA_GEMV_H
@@ -115,6 +115,11 @@ PAIA_API int paia_quantize_int4_zp_g128(const void* W, void* packed, void* scale
  * paia-bench/bench/ops/ours_bf16.py:32-38): the library's per-shape variant for kind 0 BF16, 1 FP8, 2 INT4 reference
  * format, 3 INT4 asymmetric (an index of the paia_gemv_int4 table). Always returns a valid index of that table. */
 PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
+/* no reference counterpart (for profilers and tools that name the kernel a call runs): which kernel a launch of
+ * `variant` of kind 0 BF16, 1 FP8, 2 INT4 reference format, 3 INT4 asymmetric runs at (N, K): 0 gemv_kernel,
+ * 1 gemv_kernel43 (INT4 launches whose waves make at most 7 weight loads: the bf16 (128 + q) decode), 2 gemv_kernel_xg
+ * (K beyond the LDS staging); -1 bad kind or variant, -2 bad shape. Launches nothing. */
+PAIA_API int paia_gemv_launch_kind(int kind, int N, int K, int variant);
 
 /* ---- small batch: M = 1..16 activation rows (matrix-core kernel, row-streaming kernel on the M = 1 design, and the
  * M = 1 GEMV itself at M = 1; the library picks per shape and M). No reference symbol: the reference's kernels are

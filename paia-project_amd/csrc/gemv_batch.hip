@@ -172,13 +172,14 @@ int pick_splits(int units0, int KB, int W)
     return S;
 }
 
-// LDS of the row-streaming kernel at M activation rows: M staged copies of x (+ INT4 lane sums).
+// LDS of the row-streaming kernel at M activation rows: M staged copies of x (+ INT4 lane sums), and for INT4 the
+// per-wave |x| maxima of a block of up to 16 waves (kind is the format number).
 uint64_t rows_lds(int kind, int M, int K)
 {
     const uint64_t row_bytes = kind == 0 ? 2ull * K : (kind == 1 ? (uint64_t)K : (uint64_t)K / 2);
     const uint64_t nchunks = (row_bytes + kChunkBytes - 1) / kChunkBytes;
     const uint64_t xq = kind == 0 ? 1 : (kind == 1 ? 2 : 4);
-    return (uint64_t)M * nchunks * (xq * kChunkBytes + (kind >= 2 ? kWave * 4u : 0u));
+    return (uint64_t)M * nchunks * (xq * kChunkBytes + (kind >= 2 ? kWave * 4u : 0u)) + lds_slot_bytes(kind, M, 16);
 }
 
 // The row-streaming variant for M = 2..4 (BF16 2..8): the M = 1 tuned choice's (R, U, W) when the table has that

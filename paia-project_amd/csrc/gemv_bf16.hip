@@ -21,7 +21,13 @@ int launch_bf16(GemvParams p, hipStream_t st)
     return launch_gemv<kBF16, R, U, W, S ? 2 : 0, H != 0>(p, st);
 }
 
-#define PV(R, U, W, S, H) {R, U, W, S, H, &launch_bf16<R, U, W, S, H>},
+template <int R, int U, int W, int S, int H>
+int kind_of_bf16(GemvParams p)
+{
+    return gemv_kernel_kind<kBF16, R, U, W, S ? 2 : 0, H != 0>(p);
+}
+
+#define PV(R, U, W, S, H) {R, U, W, S, H, &launch_bf16<R, U, W, S, H>, &kind_of_bf16<R, U, W, S, H>},
 #define PV_W(R, U, S, H) PV(R, U, 4, S, H) PV(R, U, 8, S, H)
 #define PV_H(R, U, S) PV_W(R, U, S, 0) PV_W(R, U, S, 1)
 #define PV_S(R, U) PV_H(R, U, 0) PV_H(R, U, 1)
@@ -56,6 +62,10 @@ namespace paia {
 int launch_gemv_bf16_picked(GemvParams p, hipStream_t st)
 {
     return kBf16Variants[paia_gemv_pick_variant(0, p.N, p.K)].fn(p, st);
+}
+int kind_bf16(int v, GemvParams p)
+{
+    return v < 0 || v >= kNumBf16 ? -1 : kBf16Variants[v].kind(p);
 }
 }  // namespace paia
 

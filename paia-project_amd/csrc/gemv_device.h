@@ -167,15 +167,74 @@ __device__ __forceinline__ float dot_i4_16B(const u32x4 w, const u32x4 x0, const
 // hold any byte b as exactly b * 2^-133: b < 128 is the subnormal b * 2^-133, b >= 128 has exponent field 1 and
 // mantissa b - 128, i.e. (1 + (b-128)/128) * 2^-126. So a nibble masked in place is q * 2^-133 in bits 0-3 and
 // 16 q * 2^-133 in bits 4-7, and v_dot2_f32_bf16 takes subnormal operands as they are (measured on gfx950, as does
-// the bf16 MFMA). With x staged as x * 2^64 against bits 0-3 and x * 2^60 against bits 4-7 every product is exactly
-// q x 2^-69 (12 significant bits), so the dot of a word is 2^-69 sum q x with no offset to remove: 5 VALU (two masks,
-// one shift, two masks) + 4 v_dot2 per 8 weights, where the 0x43-exponent decode takes 7 + 4 and leaves a
+// the bf16 MFMA). With x staged as x * 2^a against bits 0-3 and x * 2^(a-4) against bits 4-7 every product is exactly
+// q x 2^(a-133) (12 significant bits), so the dot of a word is 2^(a-133) sum q x with no offset to remove: 5 VALU (two
+// masks, one shift, two masks) + 4 v_dot2 per 8 weights, where the 0x43-exponent decode takes 7 + 4 and leaves a
 // 128 sum x term. The pairs are (q0,q4), (16q1,16q5), (q2,q6), (16q3,16q7) against x staged as
-// (x0,x4)2^64, (x1,x5)2^60, (x2,x6)2^64, (x3,x7)2^60. Exact while |x| < 2^64 (x * 2^64 stays finite) and the
-// products stay normal (|q x| >= 2^-57); outside that range an x overflows to inf or a product loses bits.
-constexpr int kI4DnXLog2 = 64;             // x scale against a nibble in bits 0-3 (bits 4-7: 2^60)
-constexpr float kI4DnUnit = 0x1p-69f;      // the dot products come out in units of 2^-69
-constexpr float kI4DnOut = 0x1p69f;        // ... so each output row is scaled back once, after its reduction
+// (x0,x4)2^a, (x1,x5)2^(a-4), (x2,x6)2^a, (x3,x7)2^(a-4).
+// The staging exponent a: 64 (the first scale, kI4StageFirst) when the activation row's largest |x| lies in
+// [2^-20, 2^64), else one picked from that largest |x| (i4_stage_exp). Both keep every staged x finite, every sum far
+// below 2^127 and the products normal down to at least 2^-37 times the largest |x| (2^-119 for the picked scale), far
+// below fp32's 2^-24 resolution of the row's terms.
+struct I4Stage {
+    int a;      // x * 2^a staged against bits 0-3 (x * 2^(a-4) against bits 4-7)
+    int unit;   // the dot products and lane sums come out in units of 2^unit, unit = a - 133
+};
+// From the largest bf16 magnitude pattern (sign cleared) of the row: exponent field e (0 for zero and subnormals
+// counts as 1, inf/NaN as 254), largest |x| < 2^(e-126), a = 253 - e: the largest staged value lies in [2^126, 2^127).
+__device__ __forceinline__ I4Stage i4_stage_exp(uint32_t max_abs_bits)
+{
+    int e = (int)(max_abs_bits >> 7);
+    e = e < 1 ? 1 : (e > 254 ? 254 : e);
+    return {253 - e, 120 - e};
+}
+constexpr I4Stage kI4StageFirst = {64, -69};
+// the first scale's window as sign-cleared bf16 patterns: largest |x| >= 2^-20 (exponent field 107) and < 2^64 (191)
+constexpr uint32_t kI4FirstLoBits = 107u << 7, kI4FirstHiBits = 191u << 7;
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(u16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// The staged pairs of one x vector (8 bf16: x0..x7 in v.x..v.w, two per word), unscaled: (x0,x4), (x1,x5), (x2,x6),
+// (x3,x7), one v_perm_b32 each.
+__device__ __forceinline__ u32x4 i4_pairs(const u32x4 v)
+{
+    return {__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+            __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+// One pair at the first scale with integer operations: each nonzero bf16's exponent field raised by E (64 or 60),
+// a packed 16-bit multiply-add of (|x| != 0) * (E << 7); zero stays zero. Exact for normal x below 2^64 (the window
+// keeps the field <= 254); a subnormal x = m 2^-133 (|x| < 2^-126) is staged as (1 + m/128) 2^-127, an absolute
+// error below 2^-126, under 2^-106 of the row's largest |x| in the window. `amax` collects the pair's |x| patterns.
+// one16 holds 0x00010001 and e16 the pair (E << 7, E << 7), both opaque to the compiler (it would otherwise turn the
+// packed minimum and multiply-add into a compare and select per half, or a shift and an add).
+__device__ __forceinline__ uint32_t i4_scale_pair_first(uint32_t p, u16x2& amax, uint32_t one16, uint32_t e16)
+{
+    const u16x2 a = as_u16x2(p & 0x7FFF7FFFu);
+    amax = __builtin_elementwise_max(amax, a);
+    const u16x2 nz = __builtin_elementwise_min(a, as_u16x2(one16));
+    return as_u32(nz * as_u16x2(e16) + as_u16x2(p));
+}
+// One pair scaled exactly by 2^a (v_ldexp_f32 per value, round trip through fp32; exact whenever the result stays a
+// normal bf16, which the picked scale ensures for every |x| above 2^-119 times the row's largest).
+__device__ __forceinline__ uint32_t i4_scale_pair_exact(uint32_t p, int a)
+{
+    const bf16x2 r = {(__bf16)__builtin_amdgcn_ldexpf(__uint_as_float(p << 16), a),
+                      (__bf16)__builtin_amdgcn_ldexpf(__uint_as_float(p & 0xFFFF0000u), a)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+// The sum of a staged vector's 8 values in the decode's units: the staged pairs dotted with the decode of an all-ones
+// word (q = 1: 2^-133 against the even pairs, 16 * 2^-133 against the odd ones), so the sum comes out exactly as the
+// products of the hot loop do. c1 = 0x00010001 and c16 = 0x00100010 are held in registers.
+__device__ __forceinline__ float i4_staged_sum(const u32x4 sx, uint32_t c1, uint32_t c16)
+{
+    float s = dot2_bf16(sx.x, c1, 0.0f);
+    s = dot2_bf16(sx.y, c16, s);
+    s = dot2_bf16(sx.z, c1, s);
+    return dot2_bf16(sx.w, c16, s);
+}
+__device__ __forceinline__ float ldexp_f32(float v, int e) { return __builtin_amdgcn_ldexpf(v, e); }
 __device__ __forceinline__ void i4_word_decode_dn(uint32_t w, uint32_t q4[4])
 {
     const uint32_t t = w >> 8;
@@ -246,6 +305,25 @@ __device__ __forceinline__ float wave_sum2(float a, float b)
     v = dpp_add<0x128, 0xF>(v);   // row_ror:8
     v = dpp_add<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
     return v;
+}
+
+// Wave maximum of non-negative values (0, the identity, fills lanes outside a DPP row mask): same steps as wave_sum,
+// lane 63 ends with the maximum.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_max(uint32_t v)
+{
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+    return v > o ? v : o;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = dpp_max<0xB1, 0xF>(v);
+    v = dpp_max<0x4E, 0xF>(v);
+    v = dpp_max<0x124, 0xF>(v);
+    v = dpp_max<0x128, 0xF>(v);
+    v = dpp_max<0x142, 0xA>(v);
+    v = dpp_max<0x143, 0xC>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 template <int CTRL>

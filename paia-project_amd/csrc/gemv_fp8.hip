@@ -26,7 +26,13 @@ int launch_fp8(GemvParams p, hipStream_t st)
     return launch_gemv<kFP8, R, U, W, kQuantAux, H != 0>(p, st);
 }
 
-#define QV(R, U, W, H) {R, U, W, 0, H, &launch_fp8<R, U, W, H>},
+template <int R, int U, int W, int H>
+int kind_of_fp8(GemvParams p)
+{
+    return gemv_kernel_kind<kFP8, R, U, W, kQuantAux, H != 0>(p);
+}
+
+#define QV(R, U, W, H) {R, U, W, 0, H, &launch_fp8<R, U, W, H>, &kind_of_fp8<R, U, W, H>},
 #define QV_W(R, U, H) QV(R, U, 4, H) QV(R, U, 8, H)
 #define QV_H(R, U) QV_W(R, U, 0) QV_W(R, U, 1)
 #define QV_U(R) QV_H(R, 1) QV_H(R, 2) QV_H(R, 4)
@@ -65,6 +71,10 @@ namespace paia {
 int launch_gemv_fp8_picked(GemvParams p, hipStream_t st)
 {
     return kFp8Variants[paia_gemv_pick_variant(1, p.N, p.K)].fn(p, st);
+}
+int kind_fp8(int v, GemvParams p)
+{
+    return v < 0 || v >= kNumFp8 ? -1 : kFp8Variants[v].kind(p);
 }
 }  // namespace paia
 

@@ -91,7 +91,13 @@ int launch_i4(GemvParams p, hipStream_t st)
     return launch_gemv<F, R, U, W, kQuantAux, H != 0>(p, st);
 }
 
-#define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4, R, U, W, H>},
+template <int F, int R, int U, int W, int H>
+int kind_of_i4(GemvParams p)
+{
+    return gemv_kernel_kind<F, R, U, W, kQuantAux, H != 0>(p);
+}
+
+#define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4, R, U, W, H>, &kind_of_i4<kI4, R, U, W, H>},
 #define QV_W(R, U, H) QV(R, U, 4, H) QV(R, U, 8, H)
 #define QV_H(R, U) QV_W(R, U, 0) QV_W(R, U, 1)
 #define QV_U(R) QV_H(R, 1) QV_H(R, 2) QV_H(R, 4)
@@ -99,7 +105,7 @@ int launch_i4(GemvParams p, hipStream_t st)
 #define QV_16 QV(1, 1, 16, 0) QV(1, 2, 16, 0) QV(1, 4, 16, 0) QV(2, 1, 16, 0) QV(2, 2, 16, 0) QV(2, 4, 16, 0)
 const Variant kInt4Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
 #undef QV
-#define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4ZP, R, U, W, H>},
+#define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4ZP, R, U, W, H>, &kind_of_i4<kI4ZP, R, U, W, H>},
 const Variant kInt4ZpVariants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
 #undef QV
 #undef QV_W
@@ -187,6 +193,10 @@ int launch_gemv_int4_picked(GemvParams p, bool zp, hipStream_t st)
 {
     const int v = paia_gemv_pick_variant(zp ? 3 : 2, p.N, p.K);
     return (zp ? kInt4ZpVariants : kInt4Variants)[v].fn(p, st);
+}
+int kind_int4(int v, bool zp, GemvParams p)
+{
+    return v < 0 || v >= kNumInt4 ? -1 : (zp ? kInt4ZpVariants : kInt4Variants)[v].kind(p);
 }
 }  // namespace paia
 

@@ -67,6 +67,12 @@ __host__ __device__ constexpr uint32_t lds_s32_bytes(int nchunks)
 {
     return (F == kI4 || F == kI4ZP) ? (uint32_t)nchunks * kWave * 4u : 0u;
 }
+// INT4 staged x: per activation row 16 bytes of per-wave window flags and one u32 slot per wave for the largest |x|
+// each wave saw (read only when the first scale does not stand), rounded to 16 bytes.
+__host__ __device__ constexpr uint32_t lds_slot_bytes(int F, int MB, int W)
+{
+    return (F == kI4 || F == kI4ZP) ? (((uint32_t)MB * 16u + (uint32_t)(MB * W) * 4u + 15u) & ~15u) : 0u;
+}
 
 // x (bf16, K values) is staged into LDS as nchunks * XQ * 64 16-byte vectors. Vector q holds x[8q .. 8q+7] (zero
 // past K) and sits at LDS index (c*XQ + j)*64 + l, where c = q / (XQ*64), l = (q mod XQ*64) / XQ, j = q mod XQ: lane
@@ -107,55 +113,133 @@ __device__ __forceinline__ float i4_pair_sum_x(u32x4& v)
     return s8;
 }
 
-// INT4, staged x for the subnormal decode (i4_word_decode_dn): the sum of the vector's 8 values (same fixed order as
-// i4_pair_sum_x), and the vector re-paired (x0,x4),(x1,x5),(x2,x6),(x3,x7) with pairs 0 and 2 scaled by 2^64 and
-// pairs 1 and 3 by 2^60 (exact: a power-of-two scale of a bf16 is a bf16 unless it overflows).
-__device__ __forceinline__ float i4_stage_x(u32x4& v)
+// INT4, staged x for the subnormal decode (i4_word_decode_dn): the vector re-paired (x0,x4),(x1,x5),(x2,x6),(x3,x7)
+// with pairs 0 and 2 scaled by 2^a and pairs 1 and 3 by 2^(a-4). FIRST: a = 64 with integer operations
+// (i4_scale_pair_first), the |x| patterns folded into amax; otherwise exactly by 2^a through fp32.
+// Constants of the INT4 staging: the lane sums' decode of q = 1 (i4_staged_sum) and the operands of
+// i4_scale_pair_first (packed ones, and the first scale's exponent increments 64 and 60 in the bf16 exponent field).
+// The last three pass through an empty asm statement (no instruction) so the compiler cannot see their values and
+// keeps the packed minimum and multiply-add packed.
+struct I4SumConsts {
+    uint32_t c1, c16, one16, e64, e60;
+    __device__ __forceinline__ I4SumConsts()
+        : c1(0x00010001u), c16(0x00100010u), one16(0x00010001u), e64(0x20002000u), e60(0x1E001E00u)
+    {
+        asm("" : "+v"(one16), "+v"(e64), "+v"(e60));
+    }
+};
+// The sum of an unscaled staged vector's 8 values (the 0x43-exponent decode's lane sums), by v_dot2 against (1, 1).
+__device__ __forceinline__ float i4_unscaled_sum(const u32x4 sx)
 {
-    const float f[8] = {bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
-                        bf16_to_f32(v.y >> 16),     bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16),
-                        bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16)};
-    const float s8 = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-    constexpr float a = 0x1p64f, b = 0x1p60f;
-    static_assert(kI4DnXLog2 == 64, "staging scales follow the decode's");
-    v.x = pack_bf16x2(f[0] * a, f[4] * a);
-    v.y = pack_bf16x2(f[1] * b, f[5] * b);
-    v.z = pack_bf16x2(f[2] * a, f[6] * a);
-    v.w = pack_bf16x2(f[3] * b, f[7] * b);
-    return s8;
+    float s = dot2_bf16(sx.x, 0x3F803F80u, 0.0f);
+    s = dot2_bf16(sx.y, 0x3F803F80u, s);
+    s = dot2_bf16(sx.z, 0x3F803F80u, s);
+    return dot2_bf16(sx.w, 0x3F803F80u, s);
 }
 
-template <int F>
-__device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32)
+// How x is staged for the INT4 kernels: for the subnormal decode at the first scale (integer operations) or at a
+// picked scale (through fp32), or unscaled for the 0x43-exponent decode.
+enum I4StageMode : int { kStageFirst = 0, kStageExact = 1, kStage43 = 2 };
+
+template <int MODE>
+__device__ __forceinline__ u32x4 i4_stage_x(const u32x4 v, int a, u16x2& amax, const I4SumConsts& k)
+{
+    if constexpr (MODE == kStage43) {
+        // (x0,x2),(x4,x6),(x1,x3),(x5,x7), the nibble order of i4_word_dot
+        return {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+    }
+    const u32x4 p = i4_pairs(v);
+    if constexpr (MODE == kStageFirst) {
+        static_assert(kI4StageFirst.a == 64, "the integer staging adds the first scale's exponents");
+        return {i4_scale_pair_first(p.x, amax, k.one16, k.e64), i4_scale_pair_first(p.y, amax, k.one16, k.e60),
+                i4_scale_pair_first(p.z, amax, k.one16, k.e64), i4_scale_pair_first(p.w, amax, k.one16, k.e60)};
+    } else {
+        return {i4_scale_pair_exact(p.x, a), i4_scale_pair_exact(p.y, a - 4), i4_scale_pair_exact(p.z, a),
+                i4_scale_pair_exact(p.w, a - 4)};
+    }
+}
+
+template <int F, int MODE = kStageFirst>
+__device__ __forceinline__ void x_put(int q, u32x4 v, u32x4* xs, float* s32, int a, u16x2& amax,
+                                      const I4SumConsts& k)
 {
     constexpr int XQ = FmtInfo<F>::kXQ;
     const int c = q / (XQ * kWave), r = q - c * (XQ * kWave);
     const int l = r / XQ, j = r - l * XQ;
     if constexpr (F == kI4 || F == kI4ZP) {
         // the 4 vectors of a lane-segment are 4 consecutive q in one quad of threads: the quad sum is the lane's
-        // 32-column x sum, (s0 + s1) + (s2 + s3), kept in the decode's units of 2^-69
-        const float s8 = quad_sum(i4_stage_x(v));
-        if (j == 0) s32[c * kWave + l] = s8 * kI4DnUnit;
+        // 32-column x sum, in the decode's units (2^(a-133) for the subnormal decode, 1 for the 0x43 decode)
+        v = i4_stage_x<MODE>(v, a, amax, k);
+        const float s8 = quad_sum(MODE == kStage43 ? i4_unscaled_sum(v) : i4_staged_sum(v, k.c1, k.c16));
+        if (j == 0) s32[c * kWave + l] = s8;
     }
     xs[(c * XQ + j) * kWave + l] = v;
 }
 
 // Store the XE early vectors, then load+store the rest. nq and NT are multiples of 4, so the `q < nq` tests are
-// uniform over each quad (quad_sum needs the whole quad).
-template <int F, int XE, int NT>
-__device__ __forceinline__ void x_store(const uint16_t* x, int K, int nchunks, const XRegs<XE>& xr, u32x4* xs,
-                                        float* s32)
+// uniform over each quad (quad_sum needs the whole quad). INT4: staged at the first scale (MODE kStageFirst: returns
+// the largest sign-cleared bf16 pattern of the vectors this thread staged, their |x| maximum; vectors past K are
+// zero) or unscaled (kStage43).
+template <int F, int XE, int NT, int MODE = kStageFirst>
+__device__ __forceinline__ uint32_t x_store(const uint16_t* x, int K, int nchunks, const XRegs<XE>& xr, u32x4* xs,
+                                            float* s32)
 {
     constexpr int XQ = FmtInfo<F>::kXQ;
     const int nq = nchunks * XQ * kWave;
     constexpr int T = NT;
+    const I4SumConsts k;
+    u16x2 amax = {0, 0};
 #pragma unroll
     for (int e = 0; e < XE; ++e) {
         const int q = (int)threadIdx.x + e * T;
-        if (q < nq) x_put<F>(q, xr.v[e], xs, s32);
+        if (q < nq) x_put<F, MODE>(q, xr.v[e], xs, s32, kI4StageFirst.a, amax, k);
     }
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)K * 2u);
-    for (int q = (int)threadIdx.x + XE * T; q < nq; q += T) x_put<F>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32);
+    for (int q = (int)threadIdx.x + XE * T; q < nq; q += T)
+        x_put<F, MODE>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32, kI4StageFirst.a, amax, k);
+    return amax.x > amax.y ? amax.x : amax.y;
+}
+
+// INT4: stage the whole row again at the scale 2^a (every vector loaded from global memory again).
+template <int F, int NT>
+__device__ __forceinline__ void x_restage(const uint16_t* x, int K, int nchunks, u32x4* xs, float* s32, int a)
+{
+    const int nq = nchunks * FmtInfo<F>::kXQ * kWave;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)K * 2u);
+    const I4SumConsts k;
+    u16x2 unused = {0, 0};
+    for (int q = (int)threadIdx.x; q < nq; q += NT)
+        x_put<F, kStageExact>(q, ld16<0>(xrs, (uint32_t)q * 16u, 0u), xs, s32, a, unused, k);
+}
+
+// INT4 first-scale window flags of one wave (one byte per wave and activation row): bit 0 some |x| >= 2^-20, bit 1
+// some |x| >= 2^64, bit 2 some x != 0. The first scale stands for the row when no wave set bit 1 and some wave set
+// bit 0, or no wave set bit 2 (all zero: every scale gives zeros).
+__device__ __forceinline__ uint32_t i4_window_flags(uint32_t tmax)
+{
+    return (__builtin_amdgcn_ballot_w64(tmax >= kI4FirstLoBits) != 0 ? 1u : 0u) |
+           (__builtin_amdgcn_ballot_w64(tmax >= kI4FirstHiBits) != 0 ? 2u : 0u) |
+           (__builtin_amdgcn_ballot_w64(tmax != 0u) != 0 ? 4u : 0u);
+}
+__device__ __forceinline__ bool i4_first_stands(uint32_t f_or)
+{
+    return (f_or & 0x02020202u) == 0u && ((f_or & 0x01010101u) != 0u || (f_or & 0x04040404u) == 0u);
+}
+// The OR of the W flag bytes at p (4-byte aligned).
+template <int W>
+__device__ __forceinline__ uint32_t or_flag_bytes(const uint8_t* p)
+{
+    static_assert(W == 4 || W == 8 || W == 16, "waves per block");
+    if constexpr (W == 4) {
+        return *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (W == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        return v.x | v.y;
+    } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        return (v.x | v.y) | (v.z | v.w);
+    }
 }
 
 // One item's registers: R*U weight loads, INT4 scales/zeros, (XG) the lane's x vectors of its U chunks, and the
@@ -208,7 +292,9 @@ struct ItemWalker {
 // accumulators per row and MB staged copies of x, so each weight is loaded and decoded once for all activation rows.
 // XG: x is not staged; each item's loads bring the lane's x vectors from global memory (L2) with the weights. For K
 // whose staged x would not fit the LDS (M = 1 only).
-template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB, bool XG = false>
+// D43 (INT4, M = 1, staged x): the 0x43-exponent decode against unscaled staged x, for launches whose waves make
+// few weight loads (launch_gemv chooses); otherwise staged INT4 x feeds the subnormal decode.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB, bool XG = false, bool D43 = false>
 __device__ __forceinline__ void gemv_body(const GemvParams& p)
 {
     static_assert(MB >= 1 && MB <= 8 && (MB <= 6 || F == kBF16 || F == kFP8) && (MB == 1 || !KSPLIT),
@@ -216,12 +302,19 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     static_assert(!XG || MB == 1, "x from global memory: M = 1 only");
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
+    static_assert(!D43 || (I4 && !XG && MB == 1), "the unscaled staged INT4 decode: M = 1 GEMV only");
+    constexpr bool DN = I4 && !XG && !D43;   // the subnormal decode against x staged at a power-of-two scale
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, then (H=1) the split-K partials
+    // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, the INT4 per-wave |x| maxima, then (H=1) the
+    // split-K partials
     const uint32_t xrow = XG ? 0u : lds_x_bytes<F>(p.nchunks), srow = XG ? 0u : lds_s32_bytes<F>(p.nchunks);
+    constexpr uint32_t slot_bytes = DN ? lds_slot_bytes(F, MB, W) : 0u;
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
     float* s32 = reinterpret_cast<float*>(smem + MB * xrow);
-    float* part = reinterpret_cast<float*>(smem + MB * xrow + MB * srow);
+    uint32_t* slots = reinterpret_cast<uint32_t*>(smem + MB * xrow + MB * srow);
+    uint8_t* flags = reinterpret_cast<uint8_t*>(slots);   // INT4: [MB][16] per-wave window flags
+    uint32_t* maxima = slots + 4 * MB;                     // INT4: [MB][W] per-wave largest |x| (second walk only)
+    float* part = reinterpret_cast<float*>(smem + MB * xrow + MB * srow + slot_bytes);
 
     const int lane = lane_id();
     const int wave = wave_id();
@@ -302,14 +395,12 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         B.chunk0 = it.s * U;
         B.k = it.k;
         B.last = !ok || it.s + it.sstep >= it.nseg;
-        // one VALU add per buffer; the u-th chunk is an immediate offset of the load
-        const uint32_t woff = lane16 + (uint32_t)B.chunk0 * kChunkBytes;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
         if constexpr (I4) {
-            // the lane's 32 weights of chunk c lie in group c*16 + gl; zero points are packed 2 groups per byte
+            // the lane's 32 weights of chunk c lie in group c*16 + gl; zero points are packed 2 groups per byte.
+            // Issued ahead of the item's weight loads: loads complete in order, so a wait for the scale or zero point
+            // never waits for the weights, wherever the compiler places the first use of either (a zero-extension
+            // of the zero-point byte at the loop head once made every item wait for its whole load set before any
+            // arithmetic).
             const uint32_t moff = gl * 2u + (uint32_t)B.chunk0 * 32u;
             const uint32_t zoff = (gl >> 1) + (uint32_t)B.chunk0 * 8u;
 #pragma unroll
@@ -320,6 +411,12 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
                     if constexpr (F == kI4ZP) B.z[r][u] = ld_u8(rz[r], zoff + (uint32_t)u * 8u, 0u);
                 }
         }
+        // one VALU add per buffer; the u-th chunk is an immediate offset of the load
+        const uint32_t woff = lane16 + (uint32_t)B.chunk0 * kChunkBytes;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r) B.w[r][u] = ld16<AUX>(rw[r], woff + (uint32_t)u * kChunkBytes, 0u);
         if constexpr (XG) {
             // the lane's x for chunk c: columns c*CC + lane*CPL .. +CPL-1 (CPL = 8*XQ), XQ 16-byte vectors; bounded
             // to K (zeros past it, and for no item at all)
@@ -343,6 +440,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
         for (int m = 0; m < MB; ++m) accm[r][m] = 0.0f;
     const int xstride = (int)(xrow / 16u);                   // u32x4 per staged x copy
     const int sstride = (int)(srow / 4u);                    // floats per staged lane-sum copy
+    I4Stage st[MB];                                          // INT4 staged x: each activation row's exponent
+#pragma unroll
+    for (int m = 0; m < MB; ++m) st[m] = {0, 0};
 
     // Chunks past the row end hold zero weights (and zero INT4 scales); their x index is clamped to the last
     // staged chunk so every product stays 0 * finite.
@@ -445,14 +545,14 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16B(B.w[r][u], xv[0], xv[1], acc[r]);
             } else {
-                // staged x: the subnormal decode, dot and x sum in units of 2^-69, no decode offset; XG: the
-                // 0x43-exponent decode against unscaled x, offset 128
+                // staged x: the subnormal decode, dot and x sum in units of 2^unit, no decode offset; XG and D43:
+                // the 0x43-exponent decode against unscaled x, offset 128
                 const float sx = XG ? sx_g : s32[c * kWave + lane];
-                constexpr float off = XG ? 128.0f : 0.0f;
+                constexpr float off = DN ? 0.0f : 128.0f;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float d = XG ? dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43)
-                                       : dot_i4dn_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3]);
+                    const float d = DN ? dot_i4dn_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3])
+                                       : dot_i4_16B(B.w[r][u], xv[0], xv[1], xv[2], xv[3], c43);
                     float s, zc;
                     if constexpr (F == kI4) {
                         s = f16_to_f32(B.s[r][u]);
@@ -487,9 +587,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
             tot[i + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
         }
         if constexpr (NV & 1) tot[NV - 1] = wave_sum(flat[NV - 1]);
-        if constexpr (I4) {   // the subnormal decode's units, 2^-69 (exact: a power of two)
+        if constexpr (DN) {   // back from the subnormal decode's units of 2^unit (exact: a power of two)
 #pragma unroll
-            for (int i = 0; i < NV; ++i) tot[i] *= kI4DnOut;
+            for (int i = 0; i < NV; ++i) tot[i] = ldexp_f32(tot[i], -st[i % MB].unit);
         }
         const int kk = B.k;
         const int r = lane - kk * R;
@@ -520,9 +620,9 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
             tot[r + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
         }
         if constexpr (R & 1) tot[R - 1] = wave_sum(acc[R - 1]);
-        if constexpr (I4 && !XG) {   // the subnormal decode's units, 2^-69 (exact: a power of two)
+        if constexpr (DN) {   // back from the subnormal decode's units of 2^unit (exact: a power of two)
 #pragma unroll
-            for (int r = 0; r < R; ++r) tot[r] *= kI4DnOut;
+            for (int r = 0; r < R; ++r) tot[r] = ldexp_f32(tot[r], -st[0].unit);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -590,11 +690,51 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(buf[d]);
     if constexpr (!XG) {
+        // INT4, subnormal decode: x is staged at the first scale (kI4StageFirst) with integer operations, and each
+        // wave parks its window flags per activation row in LDS; after the barrier every wave reads the block's (the
+        // row's: every block stages the whole row). A row whose x lies outside the first scale's window is staged
+        // again at the scale its largest |x| calls for (i4_stage_exp), behind two more barriers. The decision is the
+        // same in every wave and block. The 0x43 decode (D43) stages x unscaled and needs no window.
+        uint32_t tmax[MB];
 #pragma unroll
-        for (int m = 0; m < MB; ++m)
-            x_store<F, XE, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xr[m], xs + m * xstride,
-                                      s32 + m * sstride);
+        for (int m = 0; m < MB; ++m) {
+            tmax[m] = x_store<F, XE, W * kWave, D43 ? kStage43 : kStageFirst>(
+                p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xr[m], xs + m * xstride, s32 + m * sstride);
+            if constexpr (DN) {
+                const uint32_t f = i4_window_flags(tmax[m]);
+                if (lane == 0) flags[m * 16 + wave] = (uint8_t)f;
+                st[m] = kI4StageFirst;
+            }
+        }
         __syncthreads();
+        if constexpr (DN) {
+            bool again = false, redo[MB];
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                const uint32_t f = (uint32_t)__builtin_amdgcn_readfirstlane((int)or_flag_bytes<W>(flags + m * 16));
+                redo[m] = !i4_first_stands(f);
+                again = again || redo[m];
+            }
+            if (again) {
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    const uint32_t mw = wave_max_u32(tmax[m]);
+                    if (redo[m] && lane == 0) maxima[m * W + wave] = mw;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    if (!redo[m]) continue;
+                    uint32_t mx = 0u;
+#pragma unroll
+                    for (int w = 0; w < W; ++w) mx = max(mx, maxima[m * W + w]);
+                    st[m] = i4_stage_exp((uint32_t)__builtin_amdgcn_readfirstlane((int)mx));
+                    x_restage<F, W * kWave>(p.x + (size_t)m * (size_t)p.K, p.K, nchunks, xs + m * xstride,
+                                            s32 + m * sstride, st[m].a);
+                }
+                __syncthreads();
+            }
+        }
     }
 
     // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
@@ -648,6 +788,13 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     gemv_body<F, R, U, W, AUX, KSPLIT, 1>(p);
 }
 
+// INT4, M = 1, staged x for the 0x43-exponent decode (the launch's waves make few weight loads).
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+__global__ void __launch_bounds__(W * kWave) gemv_kernel43(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, KSPLIT, 1, false, true>(p);
+}
+
 // x from global memory (K beyond what the LDS can stage), M = 1.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 __global__ void __launch_bounds__(W * kWave) gemv_kernel_xg(GemvParams p)
@@ -691,22 +838,30 @@ constexpr uint32_t kMaxLds = 65536;
 // LDS for split-K partials (H=1): up to this much, within kMaxLds; at least one group (W*R floats) is needed.
 constexpr uint32_t kPartBytes = 8192;
 
-// LDS of a launch, and (H=1) the number of row groups per combine round. Returns 0 when the K is too large.
-template <int F, int R, int W, bool KSPLIT>
-uint32_t gemv_lds_plan(int nchunks, int* round)
+// LDS of an M = 1 launch of format F with R rows per group, W waves per block, split-K or not, and (split-K) the
+// number of row groups per combine round. Returns 0 when x does not fit (the launch then loads x from global memory).
+// The one plan both the launch and paia_gemv_pick_variant (which prefers variants that stage x) go by.
+inline uint32_t lds_plan(int F, int R, int W, bool ksplit, int nchunks, int* round)
 {
     *round = 1;
-    // x plus INT4 sums: (XQ*1024 + 256) bytes per chunk; compared in 64 bits (nchunks reaches 2^22 at K = 2^31)
-    if ((uint64_t)nchunks * (FmtInfo<F>::kXQ * kChunkBytes + ((F == kI4 || F == kI4ZP) ? kWave * 4 : 0)) > kMaxLds)
-        return 0;
-    const uint32_t base = lds_x_bytes<F>(nchunks) + lds_s32_bytes<F>(nchunks);
-    if (!KSPLIT) return base;
+    const bool i4 = F == kI4 || F == kI4ZP;
+    const uint64_t xq = F == kBF16 ? 1u : F == kFP8 ? 2u : 4u;
+    // x plus INT4 sums: (XQ*1024 + 256) bytes per chunk; 64-bit (nchunks reaches 2^22 at K = 2^31)
+    const uint64_t base64 = (uint64_t)nchunks * (xq * kChunkBytes + (i4 ? kWave * 4u : 0u)) + lds_slot_bytes(F, 1, W);
+    if (base64 > kMaxLds) return 0;
+    const uint32_t base = (uint32_t)base64;
+    if (!ksplit) return base;
     const uint32_t group_bytes = (uint32_t)(W * R * 4);
     uint32_t part = kMaxLds - base < kPartBytes ? kMaxLds - base : kPartBytes;
     part -= part % group_bytes;
     if (part < group_bytes) return 0;
     *round = (int)(part / group_bytes);
     return base + part;
+}
+template <int F, int R, int W, bool KSPLIT>
+uint32_t gemv_lds_plan(int nchunks, int* round)
+{
+    return lds_plan(F, R, W, KSPLIT, nchunks, round);
 }
 
 // Resident blocks per CU the occupancy calculator allows for a kernel (queried once per kernel).
@@ -816,20 +971,80 @@ int launch_gemv_xg(GemvParams p, hipStream_t st)
     return launch_gemv_xg_knobs<F, 1, 2, 8, AUX, true>(p, st);
 }
 
+// INT4 with staged x: launches whose waves make at most this many 16-byte weight loads run the 0x43-exponent decode
+// against unscaled x (gemv_kernel43); the others the subnormal decode. The subnormal decode takes 5 VALU per 8 weights
+// against the 0x43 decode's 7, but its staging scales x and checks the row's range before any item is consumed, a
+// prologue that precedes the first item on every wave; with few items per wave the prologue weighs more. Measured on
+// MI355X (per launch, 0x43 / subnormal decode, loads per wave in brackets): asymmetric format Llama qkv 6144x4096 (2)
+// 4.74 / 4.93 us, o 4096x4096 (2) 3.96 / 4.09, down 4096x14336 (7) 7.16 / 7.28, gate_up 28672x4096 (8) 12.11 / 12.18,
+// Qwen qkv 4608x3584 (2) 4.55 / 4.75, down 3584x18944 (10) 8.94 / 8.61, gate_up 37888x3584 (20) 14.02 / 13.35;
+// reference format down (7) 7.09 / 7.21, gate_up (8) 11.85 / 11.50.
+constexpr int kI4Max43Loads = 7;
+
+// 16-byte weight loads per wave (per lane) of a launch of `grid` blocks: the groups a wave (H=0) or block (H=1) takes,
+// times the segments a wave takes of each, times R * U loads per item.
+inline int loads_per_wave(const GemvParams& p, int grid, int R, int U, int W, bool ksplit)
+{
+    if (grid <= 0) return 0;
+    if (!ksplit) return ((p.ngroups + grid * W - 1) / (grid * W)) * p.nseg * R * U;
+    return ((p.ngroups + grid - 1) / grid) * ((p.nseg + W - 1) / W) * R * U;
+}
+
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+int gemv43_max_blocks_per_cu()
+{
+    static std::atomic<int> cached{0};
+    return max_blocks_per_cu_of(gemv_kernel43<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
+}
+
+// The kernel a launch runs: 0 gemv_kernel, 1 gemv_kernel43 (INT4, few loads per wave), 2 gemv_kernel_xg (x beyond the
+// LDS). p as the entry point fills it; sets p's derived fields and *lds, *grid for the chosen kernel.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+int gemv_plan(GemvParams& p, uint32_t* lds, int* grid)
+{
+    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
+    p.nseg = (p.nchunks + U - 1) / U;
+    p.ngroups = (p.N + R - 1) / R;
+    *lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
+    if (*lds == 0) return 2;
+    if constexpr ((F == kI4 || F == kI4ZP) && R * U <= 2) {
+        const int g43 = gemv_grid<R, W, KSPLIT>(p, *lds, gemv43_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>());
+        if (loads_per_wave(p, g43, R, U, W, KSPLIT) <= kI4Max43Loads) {
+            *grid = g43;
+            return 1;
+        }
+    }
+    *grid = gemv_grid<R, W, KSPLIT>(p, *lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>(),
+                                    F == kBF16 ? kLeadWaveBlocksPerCu : 0);
+    return 0;
+}
+
 // Launch on `st`. Arguments were validated by the caller. Returns 0 or a hipError_t. K whose staged x (and, H=1, one
 // round of partials) does not fit the LDS runs launch_gemv_xg instead.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 int launch_gemv(GemvParams p, hipStream_t st)
 {
-    p.nchunks = (int)((p.row_bytes + kChunkBytes - 1) / kChunkBytes);
-    p.nseg = (p.nchunks + U - 1) / U;
-    p.ngroups = (p.N + R - 1) / R;
-    const uint32_t lds = gemv_lds_plan<F, R, W, KSPLIT>(p.nchunks, &p.round);
-    if (lds == 0) return launch_gemv_xg<F, AUX>(p, st);
-    const int grid = gemv_grid<R, W, KSPLIT>(p, lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>(),
-                                             F == kBF16 ? kLeadWaveBlocksPerCu : 0);
+    uint32_t lds = 0;
+    int grid = 0;
+    const int k = gemv_plan<F, R, U, W, AUX, KSPLIT>(p, &lds, &grid);
+    if (k == 2) return launch_gemv_xg<F, AUX>(p, st);
+    if constexpr ((F == kI4 || F == kI4ZP) && R * U <= 2) {
+        if (k == 1) {
+            hipLaunchKernelGGL((gemv_kernel43<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
+            return (int)hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((gemv_kernel<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
     return (int)hipGetLastError();
+}
+
+// Which kernel a launch of this variant runs (gemv_plan's first result), for tools that name it.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+int gemv_kernel_kind(GemvParams p)
+{
+    uint32_t lds = 0;
+    int grid = 0;
+    return gemv_plan<F, R, U, W, AUX, KSPLIT>(p, &lds, &grid);
 }
 
 // LDS the row-streaming launch may request: the device's per-block limit (160 KiB on MI355X), at least kMaxLds. A block
@@ -849,7 +1064,8 @@ int launch_gemv_rows(GemvParams p, hipStream_t st)
     p.nseg = (p.nchunks + U - 1) / U;
     p.ngroups = (p.N + R - 1) / R;
     p.round = 1;
-    const uint64_t lds = (uint64_t)MB * (lds_x_bytes<F>(p.nchunks) + lds_s32_bytes<F>(p.nchunks));
+    const uint64_t lds = (uint64_t)MB * (lds_x_bytes<F>(p.nchunks) + lds_s32_bytes<F>(p.nchunks)) +
+                         lds_slot_bytes(F, MB, W);
     if (lds > rows_max_lds()) return -2;
     if (lds > kMaxLds) {   // beyond the default dynamic-LDS limit: raise it once for this kernel
         static std::atomic<int> raised{0};
@@ -869,6 +1085,7 @@ int launch_gemv_rows(GemvParams p, hipStream_t st)
 }
 
 using GemvLaunchFn = int (*)(GemvParams, hipStream_t);
+using GemvKindFn = int (*)(GemvParams);
 
 // The M = 1 kernel of a format with the library's variant for (N, K) (paia_gemv_pick_variant), p filled as that
 // format's M = 1 entry point fills it; 0, -2 (LDS limit) or a hipError_t. The small-batch entry points use these at
@@ -880,7 +1097,14 @@ int launch_gemv_int4_picked(GemvParams p, bool zp, hipStream_t st);
 struct Variant {
     int R, U, W, S, H;
     GemvLaunchFn fn;
+    GemvKindFn kind;   // which kernel a launch runs (gemv_kernel_kind)
 };
+
+// The kernel a launch of table variant v would run for p (N, K, row_bytes and the format's sizes filled): 0
+// gemv_kernel, 1 gemv_kernel43, 2 gemv_kernel_xg; -1 for a variant outside the table. zp: the asymmetric INT4 format.
+int kind_bf16(int v, GemvParams p);
+int kind_fp8(int v, GemvParams p);
+int kind_int4(int v, bool zp, GemvParams p);
 
 inline bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 

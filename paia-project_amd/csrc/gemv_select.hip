@@ -29,23 +29,18 @@ const Pick kTuned[] = {
     {-1, 0, 0, 0, 0, 0, 0, 0},   // end marker
 };
 
-// Whether a variant of table 0 (BF16), 1 (FP8) or 2 (INT4) stages x for this K in the LDS: the launch's LDS plan
-// (paia::gemv_lds_plan) fits, x and the INT4 lane sums plus, for split-K, one round of partial sums. A variant that
-// does not runs the x-from-global kernel instead, which is slower, so the pick prefers one that does.
+// Whether a variant of table 0 (BF16), 1 (FP8) or 2 (INT4, both formats) stages x for this K in the LDS: the launch's
+// LDS plan (paia::lds_plan, the one the launch itself goes by) fits x and the INT4 lane sums plus, for split-K, one
+// round of partial sums. A variant that does not runs the x-from-global kernel instead, which is slower, so the pick
+// prefers one that does.
 bool stages_x(int table, int R, int W, int H, int K)
 {
     using namespace paia;
     const uint64_t row_bytes = table == 0 ? 2ull * (uint64_t)K : table == 1 ? (uint64_t)K : (uint64_t)K / 2u;
     const uint64_t nchunks = (row_bytes + kChunkBytes - 1) / kChunkBytes;
-    const uint64_t xq = table == 0 ? 1u : table == 1 ? 2u : 4u;
-    const uint64_t base64 = nchunks * xq * kChunkBytes + (table == 2 ? nchunks * kWave * 4u : 0u);
-    if (base64 > kMaxLds) return false;
-    const uint32_t base = (uint32_t)base64;
-    if (!H) return true;
-    const uint32_t group = (uint32_t)(W * R * 4);
-    uint32_t part = kMaxLds - base < kPartBytes ? kMaxLds - base : kPartBytes;
-    part -= part % group;
-    return part >= group;
+    if (nchunks > (uint64_t)(kMaxLds / kChunkBytes)) return false;   // cannot fit at any format: skip the plan
+    int round = 0;
+    return lds_plan(table == 0 ? kBF16 : table == 1 ? kFP8 : kI4, R, W, H != 0, (int)nchunks, &round) != 0;
 }
 
 int find_bf16(int R, int U, int W, int S, int H)
@@ -117,6 +112,33 @@ int paia_gemv_pick_variant(int kind, int N, int K)
     if (!stages_x(table, R, W, H, K)) H = 0;
     const int v = table == 0 ? find_bf16(R, U, W, 0, H) : find_quant(table, R, U, W, H);
     return v < 0 ? 0 : v;
+}
+
+// Which kernel a launch of `variant` runs at (N, K): 0 gemv_kernel, 1 gemv_kernel43 (INT4 with few weight loads per
+// wave: the 0x43-exponent decode), 2 gemv_kernel_xg (K beyond the LDS), as a profiler names them; -1 bad kind or
+// variant, -2 bad shape. No launch; the grid sizing queries the current device once.
+int paia_gemv_launch_kind(int kind, int N, int K, int variant)
+{
+    if (kind < 0 || kind > 3) return -1;
+    if (N <= 0 || K <= 0) return -2;
+    paia::GemvParams p{};
+    p.N = N;
+    p.K = K;
+    const int G = K / 128;
+    switch (kind) {
+    case 0:
+        p.row_bytes = 2u * (uint32_t)K;
+        return paia::kind_bf16(variant, p);
+    case 1:
+        p.row_bytes = (uint32_t)K;
+        return paia::kind_fp8(variant, p);
+    default:
+        if (K & 127) return -2;
+        p.row_bytes = (uint32_t)K / 2u;
+        p.meta_bytes = (uint32_t)G * 2u;
+        p.zbytes = kind == 3 ? (uint32_t)(G + 1) / 2u : 0u;
+        return paia::kind_int4(variant, kind == 3, p);
+    }
 }
 
 }  // extern "C"

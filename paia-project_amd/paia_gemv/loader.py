@@ -7,7 +7,7 @@ torch's current stream, so calls can be captured into a HIP graph (torch.cuda.CU
 
 Additions for the gfx950 build: `bf16_bias`, `fp8_bias`, `int4_zp` (asymmetric INT4 with optional bias),
 `dequant_fp8`, `dequant_int4`, `dequant_int4_zp`, `quantize_fp8_rowwise`, `quantize_int4_g128`,
-`quantize_int4_zp_g128`, `pick_variant`, `build_info`.
+`quantize_int4_zp_g128`, `pick_variant`, `launch_kind`, `build_info`.
 """
 from __future__ import annotations
 
@@ -65,6 +65,7 @@ class GemvLib:
             "paia_quantize_int4_g128": [_P, _P, _P, _I, _I, _P],
             "paia_quantize_int4_zp_g128": [_P, _P, _P, _P, _I, _I, _P],
             "paia_gemv_pick_variant": [_I, _I, _I],
+            "paia_gemv_launch_kind": [_I, _I, _I, _I],
             "paia_gemv_bf16_variant_count": [],
             "paia_gemv_bf16_variant_info": [_I] + [ctypes.POINTER(_I)] * 5,
             "paia_gemv_batch_variant_count": [_I],
@@ -205,6 +206,16 @@ class GemvLib:
         return self._lib.paia_gemv_pick_variant(KINDS[kind], N, K)
 
     # ---- small batch (M = 1..16 activation rows, x [M,K] and y [M,N] bf16 row-major) -------------------------
+    KERNELS = ("gemv_kernel", "gemv_kernel43", "gemv_kernel_xg")
+
+    def launch_kind(self, kind, N, K, variant):
+        """The kernel a call of `variant` runs at (N, K), as a profiler names it: "gemv_kernel", "gemv_kernel43" (INT4
+        launches with few weight loads per wave) or "gemv_kernel_xg" (K beyond the LDS staging)."""
+        k = self._lib.paia_gemv_launch_kind(KINDS[kind], N, K, variant)
+        if k < 0:
+            raise ValueError(f"paia_gemv_launch_kind({kind}, {N}, {K}, {variant}) returned {k}")
+        return self.KERNELS[k]
+
     def batch_pick_variant(self, kind, M, N, K):
         """The library's default small-batch variant (an index of variants_batch[kind]); -1 if M is out of range."""
         return self._lib.paia_gemv_batch_pick_variant(KINDS[kind], M, N, K)

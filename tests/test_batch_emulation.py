@@ -228,12 +228,15 @@ ROWS_M8 = (2, 3, 4, 5, 6, 7, 8)      # BF16 and FP8 have row-streaming variants 
 ROWS_M6 = (2, 3, 4, 5, 6)            # INT4 up to 6
 
 
-def rows_lds(fmt, M, K):
-    """LDS of the row-streaming kernel (launch_gemv_rows): M staged copies of x, plus INT4 lane sums."""
+def rows_lds(fmt, M, K, W=16):
+    """LDS of the row-streaming kernel (launch_gemv_rows) with W-wave blocks: M staged copies of x, plus INT4 lane
+    sums, 16 bytes of window flags per activation row and one |x|-maximum slot per (activation row, wave), rounded to
+    16 bytes (lds_slot_bytes). W = 16 is the upper bound the library's pick uses."""
     row_bytes = {"bf16": 2 * K, "fp8": K}.get(fmt, K // 2)
     nchunks = -(-row_bytes // 1024)
     xq = {"bf16": 1, "fp8": 2}.get(fmt, 4)
-    return M * nchunks * (xq * 1024 + (256 if fmt.startswith("int4") else 0))
+    i4 = fmt.startswith("int4")
+    return M * nchunks * (xq * 1024 + (256 if i4 else 0)) + ((M * 16 + M * W * 4 + 15) // 16 * 16 if i4 else 0)
 
 
 def rows_lds_limit():
@@ -252,7 +255,7 @@ def runs(fmt, M, N, K, v, lds_limit=65536):
     if v["P"] == 0 and v["U"] == 0:
         return M == 1 and rows_lds(fmt, 1, K) + 512 <= 65536
     if v["P"] == 0:
-        return v["X"] == M and rows_lds(fmt, M, K) <= lds_limit
+        return v["X"] == M and rows_lds(fmt, M, K, v["W"]) <= lds_limit
     return plan(fmt, M, N, K, v["P"], v["U"], v["W"], v["S"], v["X"], lds_limit) is not None
 
 

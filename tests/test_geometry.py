@@ -32,8 +32,9 @@ def lds_bytes(fmt, nchunks):
 
 
 def lds_plan(fmt, nchunks, R, W, H):
-    """gemv_lds_plan: (LDS bytes, groups per combine round), or (0, 1) when K is too large."""
-    base = lds_bytes(fmt, nchunks)
+    """gemv_lds_plan: (LDS bytes, groups per combine round), or (0, 1) when K is too large. INT4 adds 16 bytes of
+    per-wave window flags and one |x|-maximum slot per wave, rounded to 16 bytes (lds_slot_bytes)."""
+    base = lds_bytes(fmt, nchunks) + ((16 + W * 4 + 15) // 16 * 16 if fmt.startswith("int4") else 0)
     if base > MAX_LDS:
         return 0, 1
     if not H:

@@ -11,9 +11,15 @@ the reference. Extra, beyond the reference's test:
   * the INT4 kernels compute s * (sum (128+q) x - (128+z) sum x), a cancellation of two terms of size ~128 |sum x|:
     zero weights with |x| ~ 100 (x ~ 100 N(0,1)) must stay within the gate;
   * the naive and unfused INT4 controls and the small-batch pick (M = 2, 4, 16) see the same operands;
-  * activations over a wide range of magnitudes: "wide" (|x| = 2^-50 .. 2^50, random signs) and "bigx" (|x| up to
-    2^62): the INT4 kernels that stage x scale it by 2^64 in bf16 to read the nibbles as bf16 subnormals, and are
-    exact for |x| < 2^64 (products q|x| >= 2^-57); these operands sit inside that range at both ends.
+  * activations over a wide range of magnitudes, random signs: "wide" (|x| = 2^-50 .. 2^50), "bigx" (2^50 .. 2^63),
+    "low" (2^-40 .. 2^-20), "tiny" (every |x| in 2^-120 .. 2^-55) and "huge" (2^60 .. 2^99, outputs still finite in
+    bf16). The INT4 kernels that stage x read the nibbles as bf16 subnormals against x scaled by a power of two: 2^64
+    when the row's largest |x| lies in [2^-20, 2^64) ("wide", "bigx" and "low" reach both ends of that window), else a
+    power each block picks from that largest |x| ("tiny", "huge": a fixed 2^64 would push the products into fp32
+    subnormals or overflow x). The reference multiplies unscaled x in fp32 (src/paia_gemv/gemv_int4.cuh:33-52), so
+    any finite x whose output is finite must pass its gate;
+  * the same extreme activations on every row-streaming INT4 variant (M = 2..6), each activation row scaled by its
+    own power of two so the rows of one call need different staging scales.
 """
 import numpy as np
 import pytest
@@ -27,14 +33,17 @@ pytestmark = pytest.mark.gpu
 
 REF_GATE = 2e-2
 N, K = 1000, 3584
+N_TALL = 12288   # INT4 range cases also at this N: most variants' waves then make more than 4 weight loads
 FORMATS = ["bf16", "fp8", "int4", "int4zp"]
+# activation exponent ranges (|x| = m * 2^e, e uniform in [lo, hi])
+EXP_RANGE = {"wide": (-50, 50), "bigx": (50, 63), "low": (-40, -20), "tiny": (-120, -55), "huge": (60, 99)}
 
 
 def variants(lib, fmt):
     return {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
 
 
-def special_operands(fmt, special, seed=5):
+def special_operands(fmt, special, seed=5, N=N):
     """CPU operands (torch tensors) of the reference's special cases for one format."""
     g = torch.Generator().manual_seed(seed)
     W = (torch.rand(N, K, generator=g) - 0.5) * 0.04
@@ -47,8 +56,8 @@ def special_operands(fmt, special, seed=5):
     elif special == "zeros_x100":       # zero weights, |x| ~ 100
         W = torch.zeros_like(W)
         x = torch.randn(K, generator=g) * 100.0
-    elif special in ("wide", "bigx"):   # |x| = m * 2^e, m in [1, 2), random signs
-        lo, hi = (-50, 50) if special == "wide" else (50, 61)
+    elif special in EXP_RANGE:          # |x| = m * 2^e, m in [1, 2), random signs
+        lo, hi = EXP_RANGE[special]
         e = torch.randint(lo, hi + 1, (K,), generator=g).double()
         sgn = torch.where(torch.rand(K, generator=g) < 0.5, -1.0, 1.0).double()
         x = (sgn * (1.0 + torch.rand(K, generator=g).double()) * torch.pow(2.0, e)).float()
@@ -81,28 +90,36 @@ def gate(oracle, fmt, np_ops, yb, what):
     return rel
 
 
-def prepared(oracle, fmt, special, cuda):
-    o = special_operands(fmt, special)
+def prepared(oracle, fmt, special, cuda, N=N):
+    o = special_operands(fmt, special, N=N)
     np_ops = as_numpy(o)
     np_ops["_ref"] = oracle_ref(oracle, fmt, np_ops)
     return o, np_ops, to_device(o, cuda)
 
 
-CASES = ([(f, sp) for f in FORMATS for sp in ("zeros", "large", "wide", "bigx")] +
-         [("int4", "zeros_x100"), ("int4zp", "zeros_x100")])
+RANGES = ("wide", "bigx", "low", "tiny", "huge")
+CASES = ([(f, sp, N) for f in FORMATS for sp in ("zeros", "large") + RANGES] +
+         [(f, sp, N_TALL) for f in ("int4", "int4zp") for sp in RANGES] +
+         [("int4", "zeros_x100", N), ("int4zp", "zeros_x100", N)])
 
 
-@pytest.mark.parametrize("fmt,special", CASES)
-def test_every_variant_on_special_operands(oracle, gemv_lib, cuda, fmt, special):
-    o, np_ops, dev = prepared(oracle, fmt, special, cuda)
+@pytest.mark.parametrize("fmt,special,n", CASES)
+def test_every_variant_on_special_operands(oracle, gemv_lib, cuda, fmt, special, n):
+    o, np_ops, dev = prepared(oracle, fmt, special, cuda, N=n)
     worst = 0.0
+    kinds = set()
     for v in variants(gemv_lib, fmt):
-        note(f"special {special} {fmt} {N}x{K} variant={v['id']}")
+        kinds.add(gemv_lib.launch_kind(fmt, n, K, v["id"]))
+        note(f"special {special} {fmt} {n}x{K} variant={v['id']}")
         yb = bits16(run_gemv(gemv_lib, fmt, dev, v["id"]))
-        worst = max(worst, gate(oracle, fmt, np_ops, yb, f"{special} {fmt} v{v}"))
+        worst = max(worst, gate(oracle, fmt, np_ops, yb, f"{special} {fmt} {n}x{K} v{v}"))
         if special == "zeros" and fmt in ("bf16", "fp8"):
             assert np.all(yb == 0), f"{fmt} v{v}: zero weights must give +0 exactly"
-    print(f"{special} {fmt}: worst {worst:.2e} over {len(variants(gemv_lib, fmt))} variants")
+    if fmt.startswith("int4") and special in RANGES:
+        # both INT4 decodes of staged x are exercised: the subnormal one at both sizes, the 0x43 one (few weight loads
+        # per wave) at the small one
+        assert "gemv_kernel" in kinds and (n != N or "gemv_kernel43" in kinds), (fmt, n, kinds)
+    print(f"{special} {fmt} {n}x{K}: worst {worst:.2e} over {len(variants(gemv_lib, fmt))} variants, {sorted(kinds)}")
 
 
 @pytest.mark.parametrize("special", ["zeros", "large", "zeros_x100"])
@@ -150,3 +167,38 @@ def test_batch_pick_on_special_operands(oracle, gemv_lib, cuda, fmt, special):
             row_ops = dict(np_ops, x=np.ascontiguousarray(xb[m]))
             row_ops["_ref"] = oracle_ref(oracle, fmt, row_ops)
             gate(oracle, fmt, row_ops, yb[m].copy(), f"batch {special} {fmt} M={M} row {m}")
+
+
+@pytest.mark.parametrize("special", ["tiny", "huge", "wide", "low"])
+@pytest.mark.parametrize("fmt", ["int4", "int4zp"])
+def test_int4_row_streaming_variants_on_extreme_x(oracle, gemv_lib, cuda, fmt, special):
+    """Every row-streaming INT4 variant (P = 0, M = 2..6) on the extreme activations, activation row m scaled by
+    2^(5m) within the range's end (so the rows of one call stage x with different scales), each row gated against
+    the fp64 oracle as the reference gates."""
+    o, np_ops, dev = prepared(oracle, fmt, special, cuda)
+    L = gemv_lib
+    rows_vs = [v for v in L.variants_batch[fmt] if v["P"] == 0 and v["U"] != 0]
+    assert rows_vs
+    sign = -1.0 if special == "huge" else 1.0       # huge: scale down, so no row leaves the finite range
+    worst = 0.0
+    for v in rows_vs:
+        M = v["X"]
+        f = torch.tensor([2.0 ** (sign * 5 * m) for m in range(M)], dtype=torch.float64)
+        xs = (o["x"].double()[None, :] * f[:, None]).to(torch.bfloat16)   # exact: powers of two
+        xd = xs.to(cuda)
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=cuda)
+        note(f"special rows {special} {fmt} M={M} variant={v}")
+        if fmt == "int4":
+            L.batch_int4(dev["Wq"].data_ptr(), dev["scales"].data_ptr(), xd.data_ptr(), y.data_ptr(), M, N, K,
+                         v["id"])
+        else:
+            L.batch_int4_zp(dev["Wq"].data_ptr(), dev["scales"].data_ptr(), dev["zeros"].data_ptr(), xd.data_ptr(),
+                            None, y.data_ptr(), M, N, K, v["id"])
+        torch.cuda.synchronize()
+        yb = bits16(y).reshape(M, N)
+        xb = xs.view(torch.int16).numpy().view(np.uint16)
+        for m in range(M):
+            row_ops = dict(np_ops, x=np.ascontiguousarray(xb[m]))
+            row_ops["_ref"] = oracle_ref(oracle, fmt, row_ops)
+            worst = max(worst, gate(oracle, fmt, row_ops, yb[m].copy(), f"rows {special} {fmt} M={M} v{v} row {m}"))
+    print(f"rows {special} {fmt}: worst {worst:.2e} over {len(rows_vs)} variants")

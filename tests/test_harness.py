@@ -173,10 +173,11 @@ def test_probe_output_setting_is_checked():
     assert P.paia_probe_set_output(None, 0) == 0
 
 
+@pytest.mark.gpu
 def test_traffic_entries_match_their_kernel(gemv_lib):
     """bench.py attaches a committed counter summary to a case only when it was measured on the kernel the case runs
     now, and every committed entry names the kernel the library picks for its case today (a retuned pick needs its
-    counters measured again)."""
+    counters measured again). On the GPU: the kernel a launch runs depends on the device's occupancy figures."""
     import bench
     d = json.loads((Path(bench.__file__).parent / "profiles" / "pmc_traffic.json").read_text())
     shapes = {bench.case_name(f, m, nm, N, K, b): (f, N, K) for _, f, m, nm, N, K, b in bench.PER_GEMV}
@@ -184,7 +185,7 @@ def test_traffic_entries_match_their_kernel(gemv_lib):
         assert bench.load_traffic(name, e["kernel"])["bytes"] == round(e["traffic_bytes"])
         assert bench.load_traffic(name, e["kernel"] + "x") is None
         f, N, K = shapes[name]
-        assert e["kernel"] == bench.kernel_name(gemv_lib, f, gemv_lib.pick_variant(f, N, K)), name
+        assert e["kernel"] == bench.kernel_name(gemv_lib, f, gemv_lib.pick_variant(f, N, K), N, K), name
 
 
 def _full_record_fixture():

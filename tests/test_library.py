@@ -180,10 +180,12 @@ def test_untuned_shapes_take_the_nearest_tuned_entry(gemv_lib):
 
 
 def _stages_x(fmt, R, W, H, K):
-    """The kernel's LDS plan (gemv_lds_plan): staged x + INT4 lane sums (+ one round of split-K partials) in 64 KiB."""
+    """The kernel's LDS plan (gemv_lds_plan): staged x + INT4 lane sums, window flags and per-wave |x| slots (+ one
+    round of split-K partials) in 64 KiB."""
     rb = {"bf16": 2 * K, "fp8": K}.get(fmt, K // 2)
     nch = -(-rb // 1024)
-    base = nch * {"bf16": 1, "fp8": 2}.get(fmt, 4) * 1024 + (nch * 256 if fmt.startswith("int4") else 0)
+    i4 = fmt.startswith("int4")
+    base = nch * {"bf16": 1, "fp8": 2}.get(fmt, 4) * 1024 + (nch * 256 + (16 + W * 4 + 15) // 16 * 16 if i4 else 0)
     if base > 65536:
         return False
     if not H:
