@@ -31,8 +31,9 @@ def test_noalloc_rejects_k_beyond_the_scratch_without_launching(gemv_lib):
 @pytest.mark.gpu
 def test_noalloc_equals_the_unfused_entry_point(oracle, gemv_lib, cuda):
     # 9000x4096: three slices of up to 4096 rows; then a smaller call (one slice) over the stale scratch; then
-    # 2500x14336: slices of 1168 rows
-    for N, K in [(9000, 4096), (1000, 3584), (2500, 14336), (8, 4096)]:
+    # 2500x14336: slices of 1168 rows; 700x65536: slices of 256 rows, the last one ragged, each slice's BF16 GEMV on
+    # the x-from-global kernel (K beyond x staging); then a small call again
+    for N, K in [(9000, 4096), (1000, 3584), (2500, 14336), (700, 65536), (8, 4096)]:
         ops, np_ops = make("int4", N, K)
         dev = to_device(ops, cuda)
         note(f"noalloc unfused reference call N={N} K={K}")
