@@ -61,22 +61,11 @@ METRIC = "µs/GEMV + achieved HBM GB/s (% of 8 TB/s), Llama-3.1-8B shapes, batch
 PEAK_GBPS = 8000.0
 B0_BYTES = 2 * 2 ** 30 - 2 ** 20   # the B0 read (the GEMV-path probe takes < 2 GiB per launch)
 
-# Every M = 1 GEMV of the BASELINE configs: (config, format, model, projection, N, K, bias)
-LLAMA = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
-QWEN = [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
-PER_GEMV = ([("configs[1]", "fp8", "llama", nm, N, K, False) for nm, N, K in LLAMA]
-            + [("configs[0]", "bf16", "llama", "o", 4096, 4096, False)]
-            + [("configs[2]", "int4zp", "llama", nm, N, K, False) for nm, N, K in LLAMA]
-            + [("configs[3]", f, "qwen", nm, N, K, nm == "qkv") for f in ("bf16", "fp8", "int4zp") for nm, N, K in QWEN]
-            + [("configs[3]", "bf16", "qwen", "lm_head", 152064, 3584, False),
-               ("configs[4]", "bf16", "llama", "lm_head", 128256, 4096, False)])
+from paia_bench.cases import BASELINE_GEMVS as PER_GEMV, LLAMA_LAYER as LLAMA, case_name, kernel_name  # noqa: E402
+
 # each format's dominant Llama GEMV (roofline_by_dtype): configs[0]'s only shape for BF16, gate_up otherwise
 DOMINANT = {"bf16": "bf16_llama_o_4096x4096", "fp8": "fp8_llama_gate_up_28672x4096",
             "int4zp": "int4zp_llama_gate_up_28672x4096"}
-
-
-def case_name(fmt, model, nm, N, K, bias):
-    return f"{fmt}_{model}_{nm}{'_bias' if bias else ''}_{N}x{K}"
 
 
 def log(msg):
@@ -227,19 +216,6 @@ def load_traffic(case_name: str, kernel: str):
                                        "over_algorithmic": e.get("traffic_over_algorithmic")}
     except (OSError, ValueError, KeyError):
         return None
-
-
-def kernel_name(lib, fmt, variant, N, K) -> str:
-    """The template instance a case launches (as rocprofv3 names it): gemv_kernel, or gemv_kernel43 for INT4 launches
-    with few weight loads per wave, with the variant's knobs; gemv_kernel_xg (its fixed knobs) for K beyond the LDS."""
-    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
-    v = fam[variant]
-    F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[fmt]
-    aux = (2 if v["S"] else 0) if fmt == "bf16" else 2
-    k = lib.launch_kind(fmt, N, K, variant)
-    if k == "gemv_kernel_xg":
-        return f"paia::gemv_kernel_xg<{F}, 1, 2, 8, {aux}, true>"
-    return f"paia::{k}<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
 
 
 def roofline_entry(lib, name, e):

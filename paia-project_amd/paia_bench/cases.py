@@ -16,6 +16,37 @@ from .inputs import make_operands, to_device
 
 REF_ROWS = 8192     # rows per chunk of the fp32 reference (paia-bench/bench/ops/cublas_bf16.py:11)
 
+# Every M = 1 GEMV of the BASELINE configs: (config, format, model, projection, N, K, bias). configs[0] BF16 o_proj,
+# configs[1] the four FP8 Llama-3.1-8B shapes, configs[2] the four INT4 (asymmetric g128) Llama shapes, configs[3] the
+# Qwen2.5-7B shapes in all three formats (qkv with its bias) and the bf16 lm_head, configs[4]'s bf16 Llama lm_head.
+LLAMA_LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+QWEN_LAYER = [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)]
+BASELINE_GEMVS = ([("configs[1]", "fp8", "llama", nm, N, K, False) for nm, N, K in LLAMA_LAYER]
+                  + [("configs[0]", "bf16", "llama", "o", 4096, 4096, False)]
+                  + [("configs[2]", "int4zp", "llama", nm, N, K, False) for nm, N, K in LLAMA_LAYER]
+                  + [("configs[3]", f, "qwen", nm, N, K, nm == "qkv") for f in ("bf16", "fp8", "int4zp")
+                     for nm, N, K in QWEN_LAYER]
+                  + [("configs[3]", "bf16", "qwen", "lm_head", 152064, 3584, False),
+                     ("configs[4]", "bf16", "llama", "lm_head", 128256, 4096, False)])
+
+
+def case_name(fmt, model, nm, N, K, bias) -> str:
+    """The name a BASELINE GEMV goes by in bench.py's record and the counter summaries."""
+    return f"{fmt}_{model}_{nm}{'_bias' if bias else ''}_{N}x{K}"
+
+
+def kernel_name(lib, fmt, variant, N, K) -> str:
+    """The template instance a call launches (as rocprofv3 names it): gemv_kernel, or gemv_kernel43 for INT4 launches
+    with few weight loads per wave, with the variant's knobs; gemv_kernel_xg (its fixed knobs) for K beyond the LDS."""
+    fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
+    v = fam[variant]
+    F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[fmt]
+    aux = (2 if v["S"] else 0) if fmt == "bf16" else 2
+    k = lib.launch_kind(fmt, N, K, variant)
+    if k == "gemv_kernel_xg":
+        return f"paia::gemv_kernel_xg<{F}, 1, 2, 8, {aux}, true>"
+    return f"paia::{k}<{F}, {v['R']}, {v['U']}, {v['W']}, {aux}, {'true' if v['H'] else 'false'}>"
+
 
 def kind_of(fmt: str) -> str:
     return "int4" if fmt.startswith("int4") else fmt

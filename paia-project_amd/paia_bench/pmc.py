@@ -8,9 +8,17 @@
         --write OUT/write/run_counter_collection.csv --out profiles/pmc_traffic.json \\
         --case fp8_gate_up_28672x4096 --fmt fp8 --shape 28672x4096
 
+    # every BASELINE GEMV in one process per counter pass (bench.py's cases, the library's picks):
+    rocprofv3 --pmc FETCH_SIZE -f csv -d OUT/fetch -o run -- python3 -m paia_bench.pmc run --all --cases-out OUT/cases.json
+    rocprofv3 --pmc WRITE_SIZE -f csv -d OUT/write -o run -- python3 -m paia_bench.pmc run --all --cases-out OUT/cases.json
+    python3 -m paia_bench.pmc summarize --all --cases OUT/cases.json --fetch OUT/fetch/run_counter_collection.csv \
+        --write OUT/write/run_counter_collection.csv --out profiles/pmc_traffic.json
+
 `run` launches, eagerly and in this order: the streaming-read probe over exactly CAL_BYTES, the copy probe over
 CAL_BYTES (reads CAL_BYTES, writes CAL_BYTES), then `reps` GEMVs of the named case rotating over enough operand
-copies (>= 4 x 256 MiB) that every weight byte comes from HBM. FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in
+copies (>= 4 x 256 MiB) that every weight byte comes from HBM. `run --all` does the same for every BASELINE GEMV in
+turn (one gated call, then `reps`) and writes the dispatch plan (case, kernel, GEMV dispatches) for `summarize --all`,
+which assigns the profiled GEMV dispatches to the cases in order and checks each one's kernel name. FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in
 KiB per dispatch; `summarize` divides each by what the same counter read for the calibration kernels (bytes counted
 per byte moved), so `traffic` is in HBM bytes of the GEMV launch, next to its algorithmic bytes.
 
@@ -33,19 +41,11 @@ from pathlib import Path
 CAL_BYTES = 256 * 2 ** 20
 
 
-def cmd_run(a) -> int:
+def _calibrate(P, cus, dev):
+    """The calibration kernels: the streaming-read probe over exactly CAL_BYTES, then the copy probe (3 times each)."""
     import torch
 
-    from paia_gemv import load_lib
     from paia_gemv.loader import current_raw_stream
-
-    from .cases import GemvCase
-    from .probe import load_probe
-    from .timing import plan_rotation
-
-    dev = torch.device("cuda:0")
-    P = load_probe()
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
     src = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
@@ -57,7 +57,61 @@ def cmd_run(a) -> int:
         if P.paia_probe_copy(src.data_ptr(), dst.data_ptr(), CAL_BYTES, cus * 8, current_raw_stream()):
             raise RuntimeError("copy probe failed")
     torch.cuda.synchronize()
-    del src, dst
+
+
+def cmd_run_all(a) -> int:
+    """Every BASELINE GEMV in turn: build its rotation, one call gated against the CPU reference, then `reps` calls."""
+    import torch
+
+    from paia_gemv import load_lib
+
+    from .cases import BASELINE_GEMVS, GemvCase, case_name, kernel_name
+    from .chain import sample_rows
+    from .probe import load_probe
+    from .timing import plan_rotation
+
+    dev = torch.device("cuda:0")
+    P = load_probe()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    _calibrate(P, cus, dev)
+    lib = load_lib()
+    plan = []
+    for cfg, fmt, model, nm, N, K, bias in BASELINE_GEMVS:
+        name = case_name(fmt, model, nm, N, K, bias)
+        c = GemvCase(lib, fmt, N, K, bias=bias, name=name)
+        n = plan_rotation(c.footprint())["n_copies"]
+        c.build(n, dev, host_copy0=False)
+        c.call(0)
+        chk = c.check_copy(0, sample_rows(N, 64))
+        if not chk["ok"]:
+            raise RuntimeError(f"{name}: correctness gate failed: {chk}")
+        for i in range(a.reps):
+            c.call((i + 1) % n)
+        torch.cuda.synchronize()
+        plan.append({"case": name, "fmt": fmt, "N": N, "K": K, "bias": bias, "variant": c.variant,
+                     "kernel": kernel_name(lib, fmt, c.variant, N, K), "dispatches": 1 + a.reps})
+        print(f"pmc run: {name} variant {c.variant} {plan[-1]['kernel']} x{1 + a.reps} over {n} copies", flush=True)
+        c.free()
+        torch.cuda.empty_cache()
+    if a.cases_out:
+        Path(a.cases_out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.cases_out).write_text(json.dumps(plan, indent=1))
+    return 0
+
+
+def cmd_run(a) -> int:
+    import torch
+
+    from paia_gemv import load_lib
+
+    from .cases import GemvCase
+    from .probe import load_probe
+    from .timing import plan_rotation
+
+    dev = torch.device("cuda:0")
+    P = load_probe()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    _calibrate(P, cus, dev)
     lib = load_lib()
     N, K = map(int, a.shape.split("x"))
     if a.batch:
@@ -75,6 +129,18 @@ def cmd_run(a) -> int:
     print(f"pmc run: {a.fmt} {N}x{K} variant {case.variant} x{a.reps} over {n} copies; "
           f"algorithmic bytes {case.bytes()['total']}", flush=True)
     return 0
+
+
+def _gemv_dispatches(path: Path, counter: str) -> list:
+    """[(short kernel name, counter value)] of the GEMV dispatches of a counter CSV, in dispatch order."""
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter or "paia::gemv" not in r["Kernel_Name"]:
+                continue
+            rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"].split("(")[0].replace("void ", ""),
+                         float(r["Counter_Value"])))
+    return [(k, v) for _, k, v in sorted(rows)]
 
 
 def _per_kernel(path: Path, counter: str) -> dict:
@@ -134,6 +200,61 @@ def cmd_summarize(a) -> int:
     return 0
 
 
+def cmd_summarize_all(a) -> int:
+    """Every case of a `run --all` plan into the summary file (entries replaced, others kept)."""
+    from paia_gemv.shapes import gemv_bytes
+
+    plan = json.loads(Path(a.cases).read_text())
+    kib = 1024.0
+    probes_f = _per_kernel(Path(a.fetch), "FETCH_SIZE")
+    probes_w = _per_kernel(Path(a.write), "WRITE_SIZE")
+    cal_read = statistics.median(probes_f["read_probe"]) * kib / CAL_BYTES
+    cal_copy_r = statistics.median(probes_f["copy_probe"]) * kib / CAL_BYTES
+    cal_copy_w = statistics.median(probes_w["copy_probe"]) * kib / CAL_BYTES
+    passes = {"fetch": _gemv_dispatches(Path(a.fetch), "FETCH_SIZE"),
+              "write": _gemv_dispatches(Path(a.write), "WRITE_SIZE")}
+    if a.dram:
+        probes_d = _per_kernel(Path(a.dram), "TCC_EA0_RDREQ_DRAM_32B_sum")
+        passes["dram"] = _gemv_dispatches(Path(a.dram), "TCC_EA0_RDREQ_DRAM_32B_sum")
+    want = sum(e["dispatches"] for e in plan)
+    for k, rows in passes.items():
+        if len(rows) != want:
+            raise SystemExit(f"{k} pass: {len(rows)} GEMV dispatches, the plan has {want}")
+    out = Path(a.out)
+    res = json.loads(out.read_text()) if out.exists() else {}
+    res["calibration"] = {"bytes": CAL_BYTES, "fetch_per_byte_read_probe": round(cal_read, 4),
+                          "fetch_per_byte_copy_probe": round(cal_copy_r, 4),
+                          "write_per_byte_copy_probe": round(cal_copy_w, 4)}
+    if a.dram:
+        res["calibration"]["dram32_bytes_per_byte_read_probe"] = round(
+            statistics.median(probes_d["read_probe"]) * 32.0 / CAL_BYTES, 4)
+    at = 0
+    for e in plan:
+        sl = {k: rows[at:at + e["dispatches"]] for k, rows in passes.items()}
+        at += e["dispatches"]
+        for k, rows in sl.items():
+            names = {n for n, _ in rows}
+            if names != {e["kernel"]}:
+                raise SystemExit(f"{e['case']}: {k} pass dispatches run {names}, the plan names {e['kernel']}")
+        # the first dispatch of each case is its gated call on copy 0: counted with the rest (same kernel, same bytes)
+        fb = statistics.median(v for _, v in sl["fetch"]) * kib / cal_read
+        wb = statistics.median(v for _, v in sl["write"]) * kib / cal_copy_w
+        alg = gemv_bytes(e["fmt"], e["N"], e["K"], e["bias"])["total"]
+        entry = {"kernel": e["kernel"], "dispatches": e["dispatches"], "fetch_bytes": round(fb),
+                 "write_bytes": round(wb), "traffic_bytes": round(fb + wb), "algorithmic_bytes": alg,
+                 "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+        if a.dram:
+            db = statistics.median(v for _, v in sl["dram"]) * 32.0
+            entry["dram_read_bytes"] = round(db)
+            entry["dram_read_over_algorithmic"] = round(db / alg, 4)
+        res.setdefault("cases", {})[e["case"]] = entry
+        print(f"{e['case']}: {e['kernel']} traffic/algorithmic {entry['traffic_over_algorithmic']}"
+              + (f", DRAM read/algorithmic {entry['dram_read_over_algorithmic']}" if a.dram else ""))
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text(json.dumps(res, indent=1) + "\n")
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -144,17 +265,27 @@ def main(argv=None) -> int:
     r.add_argument("--bias", action="store_true")
     r.add_argument("--reps", type=int, default=20)
     r.add_argument("--batch", type=int, default=0, help="M > 0: the small-batch kernels with M activation rows")
+    r.add_argument("--all", action="store_true", help="every BASELINE GEMV in turn (bench.py's cases)")
+    r.add_argument("--cases-out", default=None, help="--all: write the dispatch plan here")
     s = sub.add_parser("summarize")
+    s.add_argument("--all", action="store_true", help="every case of a `run --all` plan (--cases)")
+    s.add_argument("--cases", default=None, help="--all: the dispatch plan `run --all` wrote")
     s.add_argument("--fetch", required=True)
     s.add_argument("--write", required=True)
     s.add_argument("--dram", default=None, help="counter CSV of TCC_EA0_RDREQ_DRAM_32B_sum (optional)")
     s.add_argument("--out", required=True)
-    s.add_argument("--case", required=True, help="name the entry is stored under (bench.py's case name)")
+    s.add_argument("--case", default=None, help="name the entry is stored under (bench.py's case name)")
     s.add_argument("--fmt", default="fp8", choices=["bf16", "fp8", "int4", "int4zp"])
     s.add_argument("--shape", default="28672x4096")
     s.add_argument("--bias", action="store_true")
     a = ap.parse_args(argv)
-    return cmd_run(a) if a.cmd == "run" else cmd_summarize(a)
+    if a.cmd == "run":
+        return cmd_run_all(a) if a.all else cmd_run(a)
+    if a.all:
+        return cmd_summarize_all(a)
+    if not a.case:
+        ap.error("summarize: --case is required without --all")
+    return cmd_summarize(a)
 
 
 if __name__ == "__main__":

@@ -260,3 +260,38 @@ def test_bench_line_is_compact():
     # a run with the optional legs skipped still forms the line
     bare = dict(full, roofline=None, roofline_by_dtype={}, per_gemv={}, b0=None, chain=None, cpu_baseline=None)
     assert json.loads(json.dumps(bench.compact_line(bare)))["per_gemv"] == {}
+
+
+def test_pmc_summary_of_every_case_assigns_dispatches_in_order(tmp_path):
+    """`summarize --all`: the GEMV dispatches of a counter pass go to the plan's cases in dispatch order, each slice
+    checked against its case's kernel; a pass with a dispatch missing, or a slice running another kernel, is refused."""
+    cal_kib = pmc.CAL_BYTES / 1024
+    ka = "void paia::gemv_kernel<1, 2, 2, 4, 2, false>(paia::GemvParams)"
+    kb = "void paia::gemv_kernel43<3, 1, 1, 8, 2, false>(paia::GemvParams)"
+    plan = [{"case": "a", "fmt": "fp8", "N": 28672, "K": 4096, "bias": False, "variant": 0,
+             "kernel": "paia::gemv_kernel<1, 2, 2, 4, 2, false>", "dispatches": 3},
+            {"case": "b", "fmt": "int4zp", "N": 4096, "K": 4096, "bias": False, "variant": 0,
+             "kernel": "paia::gemv_kernel43<3, 1, 1, 8, 2, false>", "dispatches": 2}]
+    (tmp_path / "plan.json").write_text(json.dumps(plan))
+    probes = [("read_probe_kernel<1>", cal_kib / 2), ("copy_probe_kernel", cal_kib / 2)]
+    fetch, write = tmp_path / "f.csv", tmp_path / "w.csv"
+    _counter_csv(fetch, [(k, "FETCH_SIZE", v) for k, v in probes] +
+                 [(ka, "FETCH_SIZE", 57500.0)] * 3 + [(kb, "FETCH_SIZE", 4300.0)] * 2)
+    _counter_csv(write, [("read_probe_kernel<1>", "WRITE_SIZE", 0.0), ("copy_probe_kernel", "WRITE_SIZE", cal_kib)] +
+                 [(ka, "WRITE_SIZE", 112.0)] * 3 + [(kb, "WRITE_SIZE", 8.0)] * 2)
+    out = tmp_path / "t.json"
+    args = ["summarize", "--all", "--cases", str(tmp_path / "plan.json"), "--fetch", str(fetch), "--write",
+            str(write), "--out", str(out)]
+    assert pmc.main(args) == 0
+    d = json.loads(out.read_text())["cases"]
+    assert d["a"]["fetch_bytes"] == round(57500.0 * 1024 * 2) and d["a"]["dispatches"] == 3
+    assert d["b"]["kernel"] == plan[1]["kernel"] and d["b"]["write_bytes"] == 8 * 1024
+    plan[1]["kernel"] = "paia::gemv_kernel<3, 1, 1, 8, 2, false>"     # the slice runs another kernel
+    (tmp_path / "plan.json").write_text(json.dumps(plan))
+    with pytest.raises(SystemExit):
+        pmc.main(args)
+    plan[1]["dispatches"] = 3                                         # one dispatch more than the pass holds
+    plan[1]["kernel"] = "paia::gemv_kernel43<3, 1, 1, 8, 2, false>"
+    (tmp_path / "plan.json").write_text(json.dumps(plan))
+    with pytest.raises(SystemExit):
+        pmc.main(args)
