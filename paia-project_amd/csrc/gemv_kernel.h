@@ -740,7 +740,35 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
     // loop header without the other buffer's loads would make the compiler's wait counts assume those loads absent,
     // and every consume would then wait for all outstanding loads (vmcnt(0)), the prefetched item included.
-    if constexpr (!KSPLIT) {
+    // The 0x43 launches (a few items per wave) leave the loop for a drain instead, once the walk has no item left to
+    // issue: issuing the empty item's loads (size-0 descriptors, no traffic) kept the wave waiting behind every
+    // outstanding request of its CU (per-wave timestamps: a median 0.68 us between the last item and the exit on
+    // FP8 4096x4096), and the drain measured 0.08-0.27 us faster on those launches. The other kernels keep the plain
+    // loop: there the drain's second exit costs a register copy and a vmcnt(0) on the back edge, which was slower on
+    // launches with many items per wave (FP8 28672x4096 +0.67 us, INT4 37888x3584 +0.85 us).
+    if constexpr (!KSPLIT && D43) {
+        auto step = [&](const Item<F, R, U, XG>& B) {
+            consume(B);
+            if (B.last) finish(B);
+        };
+        static_assert(D == 2, "the drains below follow two buffers");
+        for (;;) {
+            if (buf[0].group < 0) return;   // a wave without items
+            step(buf[0]);
+            if (!it.valid()) goto drain0;
+            issue(buf[0]);
+            if (buf[1].group < 0) return;   // a wave with one item
+            step(buf[1]);
+            if (!it.valid()) goto drain1;
+            issue(buf[1]);
+        }
+    drain0:   // buf[0] was the walk's last but one item or none: buf[1] holds the last, if any
+        if (buf[1].group >= 0) step(buf[1]);
+        return;
+    drain1:
+        if (buf[0].group >= 0) step(buf[0]);
+        return;
+    } else if constexpr (!KSPLIT) {
         for (;;) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
