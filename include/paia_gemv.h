@@ -118,7 +118,8 @@ PAIA_API int paia_gemv_pick_variant(int kind, int N, int K);
 /* no reference counterpart (for profilers and tools that name the kernel a call runs): which kernel a launch of
  * `variant` of kind 0 BF16, 1 FP8, 2 INT4 reference format, 3 INT4 asymmetric runs at (N, K): 0 gemv_kernel,
  * 1 gemv_kernel43 (INT4 launches whose waves make at most 7 weight loads: the bf16 (128 + q) decode), 2 gemv_kernel_xg
- * (K beyond the LDS staging); -1 bad kind or variant, -2 bad shape. Launches nothing. */
+ * (K beyond the LDS staging), 3 gemv_kernel_dr and 4 gemv_kernel43_dr (0 and 1 for row-parallel launches whose waves
+ * take at most two items: the walk ends in a drain); -1 bad kind or variant, -2 bad shape. Launches nothing. */
 PAIA_API int paia_gemv_launch_kind(int kind, int N, int K, int variant);
 
 /* ---- small batch: M = 1..16 activation rows (matrix-core kernel, row-streaming kernel on the M = 1 design, and the

@@ -294,7 +294,8 @@ struct ItemWalker {
 // whose staged x would not fit the LDS (M = 1 only).
 // D43 (INT4, M = 1, staged x): the 0x43-exponent decode against unscaled staged x, for launches whose waves make
 // few weight loads (launch_gemv chooses); otherwise staged INT4 x feeds the subnormal decode.
-template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB, bool XG = false, bool D43 = false>
+// DR (M = 1, H = 0): the walk ends in a drain, for launches whose waves take at most two items (launch_gemv chooses).
+template <int F, int R, int U, int W, int AUX, bool KSPLIT, int MB, bool XG = false, bool D43 = false, bool DR = false>
 __device__ __forceinline__ void gemv_body(const GemvParams& p)
 {
     static_assert(MB >= 1 && MB <= 8 && (MB <= 6 || F == kBF16 || F == kFP8) && (MB == 1 || !KSPLIT),
@@ -303,6 +304,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     constexpr int XQ = FmtInfo<F>::kXQ;
     constexpr bool I4 = (F == kI4 || F == kI4ZP);
     static_assert(!D43 || (I4 && !XG && MB == 1), "the unscaled staged INT4 decode: M = 1 GEMV only");
+    static_assert(!DR || (!KSPLIT && MB == 1), "the drain: row-parallel M = 1 launches only");
     constexpr bool DN = I4 && !XG && !D43;   // the subnormal decode against x staged at a power-of-two scale
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // LDS: MB staged copies of x, then MB copies of the INT4 lane sums, the INT4 per-wave |x| maxima, then (H=1) the
@@ -740,13 +742,13 @@ __device__ __forceinline__ void gemv_body(const GemvParams& p)
     // The loops leave by `return` when the wave's items run out (nothing follows them): an exit that rejoined the
     // loop header without the other buffer's loads would make the compiler's wait counts assume those loads absent,
     // and every consume would then wait for all outstanding loads (vmcnt(0)), the prefetched item included.
-    // The 0x43 launches (a few items per wave) leave the loop for a drain instead, once the walk has no item left to
-    // issue: issuing the empty item's loads (size-0 descriptors, no traffic) kept the wave waiting behind every
-    // outstanding request of its CU (per-wave timestamps: a median 0.68 us between the last item and the exit on
-    // FP8 4096x4096), and the drain measured 0.08-0.27 us faster on those launches. The other kernels keep the plain
-    // loop: there the drain's second exit costs a register copy and a vmcnt(0) on the back edge, which was slower on
-    // launches with many items per wave (FP8 28672x4096 +0.67 us, INT4 37888x3584 +0.85 us).
-    if constexpr (!KSPLIT && D43) {
+    // The drain kernels (DR: launches whose waves take at most two items) leave the walk for a drain instead, once it
+    // has no item left to issue: issuing the empty item's loads (size-0 descriptors, no traffic) kept the wave
+    // waiting behind every outstanding request of its CU (per-wave timestamps: a median 0.68 us between the last
+    // item and the exit on FP8 4096x4096, 0.12 us with the drain on INT4 4096x4096). The drain loop's second exit
+    // costs a register copy and a vmcnt(0) on its back edge, which never runs at two items per wave but was slower
+    // with more (FP8 28672x4096 +0.67 us, INT4 37888x3584 +0.85 us, INT4 4096x14336 +0.11): those keep the plain loop.
+    if constexpr (!KSPLIT && DR) {
         auto step = [&](const Item<F, R, U, XG>& B) {
             consume(B);
             if (B.last) finish(B);
@@ -816,11 +818,25 @@ __global__ void __launch_bounds__(W * kWave) gemv_kernel(GemvParams p)
     gemv_body<F, R, U, W, AUX, KSPLIT, 1>(p);
 }
 
+// The same, ending in a drain (H = 0 launches whose waves take at most two items).
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+__global__ void __launch_bounds__(W * kWave) gemv_kernel_dr(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, KSPLIT, 1, false, false, true>(p);
+}
+
 // INT4, M = 1, staged x for the 0x43-exponent decode (the launch's waves make few weight loads).
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 __global__ void __launch_bounds__(W * kWave) gemv_kernel43(GemvParams p)
 {
     gemv_body<F, R, U, W, AUX, KSPLIT, 1, false, true>(p);
+}
+
+// The same, ending in a drain.
+template <int F, int R, int U, int W, int AUX, bool KSPLIT>
+__global__ void __launch_bounds__(W * kWave) gemv_kernel43_dr(GemvParams p)
+{
+    gemv_body<F, R, U, W, AUX, KSPLIT, 1, false, true, true>(p);
 }
 
 // x from global memory (K beyond what the LDS can stage), M = 1.
@@ -1025,8 +1041,26 @@ int gemv43_max_blocks_per_cu()
     return max_blocks_per_cu_of(gemv_kernel43<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
 }
 
+// Whether the drain kernel of a launch planned for its plain twin holds the same grid resident at once (the drain
+// kernels use more registers; a grid that no longer fits in one round would queue blocks behind the first round).
+template <int F, int R, int U, int W, int AUX, bool KSPLIT, bool K43>
+bool drain_fits(int grid)
+{
+    if constexpr (KSPLIT) {
+        return false;
+    } else {
+        static std::atomic<int> cached{0};
+        int per_cu = 0;
+        if constexpr (K43) per_cu = max_blocks_per_cu_of(gemv_kernel43_dr<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
+        else per_cu = max_blocks_per_cu_of(gemv_kernel_dr<F, R, U, W, AUX, KSPLIT>, W * kWave, cached);
+        const DeviceFacts df = device_facts();
+        return grid <= (df.cus > 0 ? df.cus : 256) * per_cu;
+    }
+}
+
 // The kernel a launch runs: 0 gemv_kernel, 1 gemv_kernel43 (INT4, few loads per wave), 2 gemv_kernel_xg (x beyond the
-// LDS). p as the entry point fills it; sets p's derived fields and *lds, *grid for the chosen kernel.
+// LDS), 3 gemv_kernel_dr and 4 gemv_kernel43_dr (the same two ending in a drain: H = 0, at most two items per wave).
+// p as the entry point fills it; sets p's derived fields and *lds, *grid for the chosen kernel.
 template <int F, int R, int U, int W, int AUX, bool KSPLIT>
 int gemv_plan(GemvParams& p, uint32_t* lds, int* grid)
 {
@@ -1037,14 +1071,16 @@ int gemv_plan(GemvParams& p, uint32_t* lds, int* grid)
     if (*lds == 0) return 2;
     if constexpr ((F == kI4 || F == kI4ZP) && R * U <= 2) {
         const int g43 = gemv_grid<R, W, KSPLIT>(p, *lds, gemv43_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>());
-        if (loads_per_wave(p, g43, R, U, W, KSPLIT) <= kI4Max43Loads) {
+        const int n = loads_per_wave(p, g43, R, U, W, KSPLIT);
+        if (n <= kI4Max43Loads) {
             *grid = g43;
-            return 1;
+            return !KSPLIT && n <= 2 * R * U && drain_fits<F, R, U, W, AUX, KSPLIT, true>(g43) ? 4 : 1;
         }
     }
     *grid = gemv_grid<R, W, KSPLIT>(p, *lds, gemv_max_blocks_per_cu<F, R, U, W, AUX, KSPLIT>(),
                                     F == kBF16 ? kLeadWaveBlocksPerCu : 0);
-    return 0;
+    const bool two = loads_per_wave(p, *grid, R, U, W, KSPLIT) <= 2 * R * U;   // at most two items per wave
+    return !KSPLIT && two && drain_fits<F, R, U, W, AUX, KSPLIT, false>(*grid) ? 3 : 0;
 }
 
 // Launch on `st`. Arguments were validated by the caller. Returns 0 or a hipError_t. K whose staged x (and, H=1, one
@@ -1059,6 +1095,19 @@ int launch_gemv(GemvParams p, hipStream_t st)
     if constexpr ((F == kI4 || F == kI4ZP) && R * U <= 2) {
         if (k == 1) {
             hipLaunchKernelGGL((gemv_kernel43<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
+            return (int)hipGetLastError();
+        }
+        if constexpr (!KSPLIT) {
+            if (k == 4) {
+                hipLaunchKernelGGL((gemv_kernel43_dr<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st,
+                                   p);
+                return (int)hipGetLastError();
+            }
+        }
+    }
+    if constexpr (!KSPLIT) {
+        if (k == 3) {
+            hipLaunchKernelGGL((gemv_kernel_dr<F, R, U, W, AUX, KSPLIT>), dim3(grid), dim3(W * kWave), lds, st, p);
             return (int)hipGetLastError();
         }
     }

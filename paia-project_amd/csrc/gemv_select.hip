@@ -115,8 +115,9 @@ int paia_gemv_pick_variant(int kind, int N, int K)
 }
 
 // Which kernel a launch of `variant` runs at (N, K): 0 gemv_kernel, 1 gemv_kernel43 (INT4 with few weight loads per
-// wave: the 0x43-exponent decode), 2 gemv_kernel_xg (K beyond the LDS), as a profiler names them; -1 bad kind or
-// variant, -2 bad shape. No launch; the grid sizing queries the current device once.
+// wave: the 0x43-exponent decode), 2 gemv_kernel_xg (K beyond the LDS), 3 gemv_kernel_dr / 4 gemv_kernel43_dr (0 / 1
+// ending in a drain: at most two items per wave), as a profiler names them; -1 bad kind or variant, -2 bad shape. No
+// launch; the grid sizing queries the current device once.
 int paia_gemv_launch_kind(int kind, int N, int K, int variant)
 {
     if (kind < 0 || kind > 3) return -1;

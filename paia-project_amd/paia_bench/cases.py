@@ -37,7 +37,8 @@ def case_name(fmt, model, nm, N, K, bias) -> str:
 
 def kernel_name(lib, fmt, variant, N, K) -> str:
     """The template instance a call launches (as rocprofv3 names it): gemv_kernel, or gemv_kernel43 for INT4 launches
-    with few weight loads per wave, with the variant's knobs; gemv_kernel_xg (its fixed knobs) for K beyond the LDS."""
+    with few weight loads per wave (either with the suffix _dr when no wave takes more than two items), with the
+    variant's knobs; gemv_kernel_xg (its fixed knobs) for K beyond the LDS."""
     fam = {"bf16": lib.variants, "fp8": lib.variants_fp8}.get(fmt, lib.variants_int4)
     v = fam[variant]
     F = {"bf16": 0, "fp8": 1, "int4": 2, "int4zp": 3}[fmt]

@@ -206,7 +206,7 @@ class GemvLib:
         return self._lib.paia_gemv_pick_variant(KINDS[kind], N, K)
 
     # ---- small batch (M = 1..16 activation rows, x [M,K] and y [M,N] bf16 row-major) -------------------------
-    KERNELS = ("gemv_kernel", "gemv_kernel43", "gemv_kernel_xg")
+    KERNELS = ("gemv_kernel", "gemv_kernel43", "gemv_kernel_xg", "gemv_kernel_dr", "gemv_kernel43_dr")
 
     def launch_kind(self, kind, N, K, variant):
         """The kernel a call of `variant` runs at (N, K), as a profiler names it: "gemv_kernel", "gemv_kernel43" (INT4

@@ -76,6 +76,7 @@ def test_real_shapes_picked_and_default_variant(oracle, gemv_lib, cuda, fmt):
     kind = fmt
     default = {"bf16": (2, 4, 4, 0, 1), "fp8": (2, 2, 4, 0, 1)}.get(fmt, (4, 2, 4, 0, 1))
     vdef = next(v["id"] for v in variants(gemv_lib, fmt) if (v["R"], v["U"], v["W"], v["S"], v["H"]) == default)
+    kinds = set()
     for N, K in sorted(set(REAL + BASELINE_SHAPES)):
         if K % kmult:
             continue
@@ -83,9 +84,12 @@ def test_real_shapes_picked_and_default_variant(oracle, gemv_lib, cuda, fmt):
         dev = to_device(ops, cuda)
         for vid in sorted({gemv_lib.pick_variant(kind, N, K), vdef}):
             note(f"{fmt} N={N} K={K} variant={vid}")
+            kinds.add(gemv_lib.launch_kind(fmt, N, K, vid))
             y = run_gemv(gemv_lib, fmt, dev, vid)
             torch.cuda.synchronize()
             check(oracle, fmt, np_ops, y, f"{fmt} {N}x{K} v{vid}")
+    # both ends of the row-parallel walk ran: the plain loop (more than two items per wave) and the drain
+    assert kinds & {"gemv_kernel", "gemv_kernel43"} and kinds & {"gemv_kernel_dr", "gemv_kernel43_dr"}, kinds
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "fp8", "int4zp"])
