@@ -15,6 +15,10 @@
 //   each thread or wave its equal share when its reads are done (the cheapest time to write them: a GEMV that writes
 //   a row group's outputs as the group completes cannot do better). The benchmark's "I/O floor" of a GEMV: its
 //   weight bytes read and its outputs written.
+// paia_probe_read_staged: the grid-stride read (unroll 1) of 256-thread blocks that each first stage xbytes of a
+//   second buffer into LDS behind a block barrier, as every block of a GEMV stages x before its first item, and read
+//   one staged vector per loaded one. The floor of a read that must stage x first: what a GEMV of these bytes and
+//   this K (xbytes = 2K) cannot beat with x in LDS.
 // paia_probe_copy: a plain 16-byte-per-lane copy of known size, the calibration kernel for the rocprofv3 byte counters
 //   (FETCH_SIZE should read its size once, WRITE_SIZE its size once).
 // paia_probe_empty: an empty kernel, for the per-launch floor of back-to-back launches in a graph.
@@ -145,6 +149,25 @@ __global__ void __launch_bounds__(256) copy_probe_kernel(const u32x4* __restrict
         __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+__global__ void __launch_bounds__(256) staged_read_kernel(const u32x4* __restrict__ p, size_t n16, uint32_t* sink,
+                                                          const u32x4* __restrict__ x, uint32_t nx16)
+{
+    extern __shared__ u32x4 xs[];
+    for (uint32_t j = threadIdx.x; j < nx16; j += blockDim.x) xs[j] = x[j];
+    __syncthreads();
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    uint32_t j = threadIdx.x % nx16;   // the staged vector read with each load: walks x, 64 vectors a step
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+        const u32x4 v = __builtin_nontemporal_load(p + i);
+        const u32x4 xv = xs[j];
+        j += 64u;
+        j = j >= nx16 ? j - nx16 : j;   // nx16 >= 64, so one subtraction keeps j < nx16
+        acc ^= (v.x ^ v.y ^ v.z ^ v.w) + (xv.x ^ xv.w);
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never true; keeps the loads alive
+}
+
 __global__ void empty_kernel() {}
 
 }  // namespace
@@ -171,6 +194,19 @@ __attribute__((visibility("default"))) int paia_probe_read(const void* buf, size
     default: return -1;
     }
 #undef READ_CASE
+    return (int)hipGetLastError();
+}
+
+// x: xbytes (1024..65536, a multiple of 16, 16-byte aligned) staged into LDS by every block first.
+__attribute__((visibility("default"))) int paia_probe_read_staged(const void* buf, size_t nbytes, void* sink, int grid,
+                                                                  const void* x, int xbytes, void* stream)
+{
+    if (!buf || !sink || !x || (reinterpret_cast<uintptr_t>(buf) & 15) || (reinterpret_cast<uintptr_t>(x) & 15) ||
+        grid <= 0 || xbytes < 1024 || xbytes > 65536 || (xbytes & 15))
+        return -2;
+    hipLaunchKernelGGL(staged_read_kernel, dim3(grid), dim3(256), (uint32_t)xbytes, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(buf), nbytes / 16, static_cast<uint32_t*>(sink),
+                       static_cast<const u32x4*>(x), (uint32_t)xbytes / 16u);
     return (int)hipGetLastError();
 }
 

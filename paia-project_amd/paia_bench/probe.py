@@ -8,6 +8,13 @@
   * B0 at the GEMV sizes: reads of S bytes from distinct slices of a 2 GiB buffer, back to back in one graph (the
     same cold-cache rotation the GEMV timings use), so "us for S bytes" is the floor a GEMV of S bytes can reach.
   * launch floor: back-to-back empty kernels in one graph.
+
+    python -m paia_bench.probe --staged [--out PATH]
+
+  * staged floor: the grid-stride read of each BASELINE GEMV's bytes by blocks that first stage 2K bytes (the GEMV's
+    x) into LDS behind a barrier, as every GEMV block must before its first item; best over 2-16 blocks per CU, timed
+    as the GEMVs are. Beside the read floor it separates what staging x costs any kernel of that shape from what the
+    GEMV's own walk costs.
 """
 from __future__ import annotations
 
@@ -35,6 +42,9 @@ def load_probe():
     lib.paia_probe_set_output.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     lib.paia_probe_copy.restype = ctypes.c_int
     lib.paia_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    lib.paia_probe_read_staged.restype = ctypes.c_int
+    lib.paia_probe_read_staged.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     lib.paia_probe_empty.restype = ctypes.c_int
     lib.paia_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
     return lib
@@ -158,6 +168,58 @@ def b0_sized(P, buf, sink, cus, S: int, configs=SIZED_CONFIGS, y=None, nout: int
     return out
 
 
+STAGED_BLOCKS_PER_CU = (2, 4, 8, 16)
+
+
+def staged_floor(P, buf, sink, x, cus, S: int, xbytes: int) -> dict:
+    """µs per read of S bytes whose blocks first stage xbytes of x into LDS (paia_probe_read_staged), over the slices
+    of `buf` as b0_sized rotates them, best over STAGED_BLOCKS_PER_CU, timed as the GEMVs are."""
+    from paia_gemv.loader import current_raw_stream
+
+    from .timing import time_per_call_us
+    S16, n = slice_plan(buf.numel(), S)
+    slices = [buf.data_ptr() + j * S16 for j in range(n)]
+    best = None
+    for b in STAGED_BLOCKS_PER_CU:
+        def call(i, b=b):
+            rc = P.paia_probe_read_staged(slices[i % n], S, sink.data_ptr(), cus * b, x.data_ptr(), xbytes,
+                                          current_raw_stream())
+            if rc:
+                raise RuntimeError(f"staged probe rc {rc}")
+        us = time_per_call_us(call, n)["us"]
+        if best is None or us < best[0]:
+            best = (us, b)
+    return {"bytes": S, "x_bytes": xbytes, "us": best[0], "blocks_per_cu": best[1]}
+
+
+def main_staged(out=None) -> int:
+    import torch
+
+    from paia_gemv.shapes import LAYER, gemv_bytes
+    P = load_probe()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    buf = torch.empty(2 * 2 ** 30 - 2 ** 20, dtype=torch.uint8, device=dev)
+    buf.random_(0, 255)
+    x = torch.empty(65536, dtype=torch.uint8, device=dev)
+    x.random_(0, 255)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    res = {"cus": cus, "staged": {}}
+    for fmt in ("bf16", "fp8", "int4zp"):
+        for nm, N, K in LAYER["llama31_8b"] + LAYER["qwen25_7b"]:
+            if 2 * K > 65536:
+                continue
+            key = f"{fmt}_{N}x{K}"
+            r = staged_floor(P, buf, sink, x, cus, gemv_bytes(fmt, N, K)["total"], 2 * K)
+            res["staged"][key] = r
+            print(f"[staged] {key:22s} {r['bytes'] / 2**20:8.2f} MiB  x {r['x_bytes']:6d} B  {r['us']:7.2f} us "
+                  f"({r['blocks_per_cu']} blocks/CU)", flush=True)
+    if out:
+        Path(out).parent.mkdir(parents=True, exist_ok=True)
+        Path(out).write_text(json.dumps(res, indent=1))
+    return 0
+
+
 def main(argv=None):
     import torch
 
@@ -168,7 +230,10 @@ def main(argv=None):
 
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=None)
+    ap.add_argument("--staged", action="store_true", help="only the staged floors of the BASELINE GEMVs")
     a = ap.parse_args(argv)
+    if a.staged:
+        return main_staged(a.out)
     P = load_probe()
     dev = torch.device("cuda:0")
     cus = torch.cuda.get_device_properties(0).multi_processor_count

@@ -173,6 +173,20 @@ def test_probe_output_setting_is_checked():
     assert P.paia_probe_set_output(None, 0) == 0
 
 
+def test_staged_probe_argument_checks():
+    """The staged-x read probe refuses null or unaligned buffers and x sizes outside 1024..65536 bytes or not a
+    multiple of 16, before any GPU work."""
+    from paia_bench.probe import load_probe
+    P = load_probe()
+    assert P.paia_probe_read_staged(None, 1 << 20, 16, 256, 16, 8192, None) == -2
+    assert P.paia_probe_read_staged(16, 1 << 20, 16, 256, None, 8192, None) == -2
+    assert P.paia_probe_read_staged(8, 1 << 20, 16, 256, 16, 8192, None) == -2     # buffer not 16-byte aligned
+    assert P.paia_probe_read_staged(16, 1 << 20, 16, 256, 16, 512, None) == -2     # x below 1024 bytes
+    assert P.paia_probe_read_staged(16, 1 << 20, 16, 256, 16, 8200, None) == -2    # not a multiple of 16
+    assert P.paia_probe_read_staged(16, 1 << 20, 16, 256, 16, 65552, None) == -2   # above 64 KiB
+    assert P.paia_probe_read_staged(16, 1 << 20, 16, 0, 16, 8192, None) == -2      # no blocks
+
+
 @pytest.mark.gpu
 def test_traffic_entries_match_their_kernel(gemv_lib):
     """bench.py attaches a committed counter summary to a case only when it was measured on the kernel the case runs
