@@ -80,9 +80,9 @@ __host__ __device__ constexpr uint32_t lds_slot_bytes(int F, int MB, int W)
 // conflict-free ds_read_b128s.
 //
 // Staging is split in two so the x loads go to memory ahead of the weight loads: x_load issues the block's first
-// XE vectors per thread (buffer loads bounded to K: zeros past K, no branch), the caller then issues its first weight
-// loads, and x_store writes them to LDS, waiting only for the x loads. Vectors beyond XE per thread (large K) are
-// loaded and stored afterwards.
+// XE vectors per thread (buffer loads bounded to K: zeros past K; INT4 skips them), the caller then issues its first
+// weight loads, and x_store writes them to LDS, waiting only for the x loads. Vectors beyond XE per thread (large K)
+// are loaded and stored afterwards.
 template <int XE>
 struct XRegs {
     u32x4 v[XE];
@@ -125,9 +125,6 @@ __device__ __forceinline__ float i4_pair_sum_x(u32x4& v)
     return s8;
 }
 
-// INT4, staged x for the subnormal decode (i4_word_decode_dn): the vector re-paired (x0,x4),(x1,x5),(x2,x6),(x3,x7)
-// with pairs 0 and 2 scaled by 2^a and pairs 1 and 3 by 2^(a-4). FIRST: a = 64 with integer operations
-// (i4_scale_pair_first), the |x| patterns folded into amax; otherwise exactly by 2^a through fp32.
 // Constants of the INT4 staging: the lane sums' decode of q = 1 (i4_staged_sum) and the operands of
 // i4_scale_pair_first (packed ones, and the first scale's exponent increments 64 and 60 in the bf16 exponent field).
 // The last three pass through an empty asm statement (no instruction) so the compiler cannot see their values and
@@ -153,6 +150,10 @@ __device__ __forceinline__ float i4_unscaled_sum(const u32x4 sx)
 // picked scale (through fp32), or unscaled for the 0x43-exponent decode.
 enum I4StageMode : int { kStageFirst = 0, kStageExact = 1, kStage43 = 2 };
 
+// INT4, staged x for the subnormal decode (i4_word_decode_dn): the vector re-paired (x0,x4),(x1,x5),(x2,x6),(x3,x7)
+// with pairs 0 and 2 scaled by 2^a and pairs 1 and 3 by 2^(a-4). kStageFirst: a = 64 with integer operations
+// (i4_scale_pair_first), the |x| patterns folded into amax; kStageExact: exactly by 2^a through fp32; kStage43: only
+// re-paired, unscaled.
 template <int MODE>
 __device__ __forceinline__ u32x4 i4_stage_x(const u32x4 v, int a, u16x2& amax, const I4SumConsts& k)
 {
