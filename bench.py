@@ -32,7 +32,7 @@ aggregate algorithmic GB/s of the FP8 layer step, plus
   chain             BASELINE configs[4]: 32 layers x 4 GEMVs + bf16 lm_head as one hipGraph, INT4 (asymmetric g128)
                     and FP8: [us per token-step, GB/s, % of 8 TB/s]; layer 0 gated before capture, layers 0, 1, 31
                     and the head after the replays (skipped with --no-chain)
-  cpu_baseline      the reference's CPU path (BASELINE.md section 3): the paia_gemv.quant torch dequantisation
+  cpu_baseline      the reference's CPU path: the paia_gemv.quant torch dequantisation
                     (src/paia_gemv/quant.py semantics) and a torch fp32 matmul (paia-bench/bench/ops/ours_quant.py:
                     69-71) on the host cores, for every GEMV of the BASELINE configs, timed (i) dequant + matmul and
                     (ii) matmul on pre-dequantised weights, median of 5 after 2 warm-ups; value = the FP8 layer
@@ -122,7 +122,7 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(budget_s: float = 90.0) -> dict:
-    """The reference's CPU path, BASELINE.md section 3, for every GEMV of the BASELINE configs (PER_GEMV, in its
+    """The reference's CPU path for every GEMV of the BASELINE configs (PER_GEMV, in its
     order): the seeded operands of the GPU run (paia_bench.inputs.make_operands, CPU generator seeded 1000 + N + K),
     dequantised with paia_gemv.quant's torch definitions (the formulas of src/paia_gemv/quant.py:16-17,34-38; (q - z) * s
     for the asymmetric INT4 format; bf16 -> fp32 for BF16) and multiplied x.float() @ Wdeq.t() in fp32

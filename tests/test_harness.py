@@ -253,12 +253,12 @@ def _full_record_fixture():
 
 
 def test_bench_line_is_compact():
-    """The one JSON line the driver parses stays under 4 KB with every field a full run fills (the round whose line
-    was 21.5 KB arrived truncated and unparsed), carries the contract keys, the dominant kernel's roofline with its
+    """The one JSON line the driver parses stays under 4 KB with every field a full run fills (a 21.5 KB line
+    arrives truncated and unparsed), carries the contract keys, the dominant kernel's roofline with its
     traffic, one roofline per format, every per-GEMV case and the CPU baseline summary."""
     import bench
     full = _full_record_fixture()
-    line = json.dumps(bench.compact_line(full, "gpurun_out/bench_report.json"))
+    line = json.dumps(bench.compact_line(full, "out/bench_report.json"))
     assert len(line) < 4096, len(line)
     out = json.loads(line)
     for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",

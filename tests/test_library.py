@@ -148,7 +148,7 @@ def test_torch_ops_registered_and_meta_shapes():
 
 
 def test_byte_accounting_matches_baseline_table():
-    """BASELINE.md section 2 figures (BF16 2NK+2K+2N; FP8 NK+4N+2K+2N; INT4 NK/2+2NG+NG/2+2K+2N; +2N with bias)."""
+    """The algorithmic bytes per GEMV (BF16 2NK+2K+2N; FP8 NK+4N+2K+2N; INT4 NK/2+2NG+NG/2+2K+2N; +2N with bias)."""
     from paia_gemv.shapes import gemv_bytes
     assert gemv_bytes("bf16", 4096, 4096)["total"] == 33_570_816
     assert gemv_bytes("fp8", 6144, 4096)["total"] == 25_210_880
