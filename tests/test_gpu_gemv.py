@@ -172,6 +172,54 @@ def test_unit_vector_exact_full_size(oracle, gemv_lib, cuda, fmt):
             assert bad.size == 0, f"{fmt} {N}x{K} k={k}: {bad.size} rows differ, first {bad[:5]}"
 
 
+@pytest.mark.parametrize("N,K", [(512, 1024), (300, 3584)])
+def test_fp8_every_code_every_variant_exact(oracle, gemv_lib, cuda, N, K):
+    """Every finite e4m3 code (the 14 subnormal codes and both zeros included) through every FP8 variant and the
+    batch picks, bit for bit: W[r, j] = code (r + j) mod 256, row scales 2^((r mod 9) - 4), and x = e_k give
+    y[r] = bf16(deq(W[r, k]) * scale[r]) (exact: at most 4 significant bits times a power of two). The two NaN codes
+    are replaced by zeros (0 * NaN in the other columns would make every row NaN); zeros are compared without their
+    sign (-0 plus the other columns' +0 products is +0)."""
+    codes = ((np.arange(N)[:, None] + np.arange(K)[None, :]) % 256).astype(np.uint8)
+    codes[codes == 0x7F] = 0x00
+    codes[codes == 0xFF] = 0x80
+    scale = (2.0 ** ((np.arange(N) % 9) - 4)).astype(np.float32)
+    dev = to_device({"fmt": "fp8", "N": N, "K": K, "Wq": torch.from_numpy(codes), "scale": torch.from_numpy(scale)},
+                    cuda)
+
+    def want_col(k):
+        k0 = k - k % 16
+        w = oracle.f32_to_bf16_bits(oracle.dequant_fp8(codes[:, k0:k0 + 16].copy(), scale)[:, k % 16])
+        return np.where((w & 0x7FFF) == 0, 0, w)
+
+    def zeroless(y):
+        y = bits16(y)
+        return np.where((y & 0x7FFF) == 0, 0, y)
+
+    ks = sorted({0, 1, 127, 255, K // 2 + 3, K - 1})
+    for k in ks:
+        x = torch.zeros(K, dtype=torch.bfloat16, device=cuda)
+        x[k] = 1.0
+        want = want_col(k)
+        d = dict(dev, x=x)
+        for v in variants(gemv_lib, "fp8"):
+            note(f"fp8 every code N={N} K={K} k={k} variant={v}")
+            bad = np.nonzero(zeroless(run_gemv(gemv_lib, "fp8", d, v["id"])) != want)[0]
+            assert bad.size == 0, f"fp8 {N}x{K} k={k} v{v}: {bad.size} rows differ, first {bad[:5]}"
+    for M in (2, 5, 8, 16):
+        kk = [ks[m % len(ks)] for m in range(M)]
+        xm = torch.zeros(M, K, dtype=torch.bfloat16)
+        for m, k in enumerate(kk):
+            xm[m, k] = 1.0
+        xm = xm.to(cuda)
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=cuda)
+        note(f"fp8 every code batch M={M} N={N} K={K}")
+        gemv_lib.batch_fp8(dev["Wq"].data_ptr(), dev["scale"].data_ptr(), xm.data_ptr(), None, y.data_ptr(), M, N, K,
+                           -1)
+        for m, k in enumerate(kk):
+            bad = np.nonzero(zeroless(y[m]) != want_col(k))[0]
+            assert bad.size == 0, f"fp8 batch M={M} {N}x{K} row {m} k={k}: {bad.size} rows differ, first {bad[:5]}"
+
+
 def test_lm_head_bf16_sampled_rows(oracle, gemv_lib, cuda):
     """The bf16 lm_heads ([4]); fp64 check on sampled rows (gemv_bf16_check.cu:79-83)."""
     rng = np.random.default_rng(11)
