@@ -2,9 +2,9 @@
 // Drop-in for src/paia_gemv/gemv_quant.cu:61-68 (same symbols, return codes and argument contract).
 //
 // Weights are OCP e4m3fn bytes [N][K] with one fp32 scale per row: y[n] = bf16_rn(scale[n] * sum_k e4m3(W[n,k]) x[k]).
-// The decode is the gfx950 e4m3 -> f32 convert, packed to bf16 pairs (exact for every code). Codes 0x7F/0xFF are NaN in e4m3fn and
-// decode to NaN here, as the reference's dequantiser defines them (quant_host.h:19, quant.py:16-17); the quantiser
-// never emits them.
+// The decode is gfx950's e4m3 -> bf16 pair convert (v_cvt_scalef32_pk_bf16_fp8 at scale 1, exact for every code).
+// Codes 0x7F/0xFF are NaN in e4m3fn and decode to NaN here, as the reference's dequantiser defines them
+// (quant_host.h:19, quant.py:16-17); the quantiser never emits them.
 //
 // Variant knobs on gfx950 (reference tuple shape R,U,W,H; S is reported as 0 and the loads are always "nt"):
 //   R rows per wave {1,2,4}, U 16-byte loads per row per batch {1,2,4}, W waves per block {4,8},
