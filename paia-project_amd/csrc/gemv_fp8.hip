@@ -8,7 +8,8 @@
 //
 // Variant knobs on gfx950 (reference tuple shape R,U,W,H; S is reported as 0 and the loads are always "nt"):
 //   R rows per wave {1,2,4}, U 16-byte loads per row per batch {1,2,4}, W waves per block {4,8},
-//   H split-K inside the block {0,1}; plus W = 16 (one block per CU) with R {1,2}, U {1,2,4}, H 0.
+//   H split-K inside the block {0,1}; plus W = 16 (one block per CU) with R {1,2}, U {1,2,4}, H 0; plus R 1, U 2,
+//   W {6,12}, H 0 (whole blocks per CU on the small BASELINE shapes).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,12 +39,16 @@ int kind_of_fp8(GemvParams p)
 #define QV_U(R) QV_H(R, 1) QV_H(R, 2) QV_H(R, 4)
 // one 16-wave block per CU (row-parallel only), appended so the indices above stay stable
 #define QV_16 QV(1, 1, 16, 0) QV(1, 2, 16, 0) QV(1, 4, 16, 0) QV(2, 1, 16, 0) QV(2, 2, 16, 0) QV(2, 4, 16, 0)
-const Variant kFp8Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_16};
+// block sizes that make the small BASELINE shapes a whole number of blocks per CU (row-parallel only; appended after
+// the W = 16 ones): 4608 rows in 768 blocks of 6, 6144 rows in 512 blocks of 12
+#define QV_WB QV(1, 2, 6, 0) QV(1, 2, 12, 0)
+const Variant kFp8Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_16 QV_WB};
 #undef QV
 #undef QV_W
 #undef QV_H
 #undef QV_U
 #undef QV_16
+#undef QV_WB
 constexpr int kNumFp8 = (int)(sizeof(kFp8Variants) / sizeof(kFp8Variants[0]));
 
 int gemv_fp8_impl(const void* Wq, const void* scale, const void* x, const void* bias, void* y, int N, int K,

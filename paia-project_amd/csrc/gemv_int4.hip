@@ -10,8 +10,9 @@
 //   paia_gemv_int4_zp       fused kernel, same variant table as paia_gemv_int4
 //
 // Variant knobs on gfx950: R rows per wave {1,2,4,8}, U 16-byte loads per row per batch {1,2,4}, W waves per block
-// {4,8}, H split-K inside the block {0,1}; plus W = 16 (one block per CU) with R {1,2}, U {1,2,4}, H 0. Weight loads
-// are always "nt" (S reported as 0).
+// {4,8}, H split-K inside the block {0,1}; plus W = 16 (one block per CU) with R {1,2}, U {1,2,4}, H 0; plus U 1, H 0
+// with (R, W) (1,9), (2,9), (1,12), (1,14) (whole blocks per CU on the small BASELINE shapes). Weight loads are always
+// "nt" (S reported as 0).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -103,15 +104,20 @@ int kind_of_i4(GemvParams p)
 #define QV_U(R) QV_H(R, 1) QV_H(R, 2) QV_H(R, 4)
 // one 16-wave block per CU (row-parallel only), appended so the indices above stay stable
 #define QV_16 QV(1, 1, 16, 0) QV(1, 2, 16, 0) QV(1, 4, 16, 0) QV(2, 1, 16, 0) QV(2, 2, 16, 0) QV(2, 4, 16, 0)
-const Variant kInt4Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
+// block sizes that make the small BASELINE shapes a whole number of blocks per CU (row-parallel only; appended after
+// the W = 16 ones): 4608 rows in 512 blocks of 9 (R = 1) or 256 of 9 (R = 2), 6144 rows in 512 blocks of 12, 3584
+// rows in 256 blocks of 14
+#define QV_WB QV(1, 1, 9, 0) QV(2, 1, 9, 0) QV(1, 1, 12, 0) QV(1, 1, 14, 0)
+const Variant kInt4Variants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16 QV_WB};
 #undef QV
 #define QV(R, U, W, H) {R, U, W, 0, H, &launch_i4<kI4ZP, R, U, W, H>, &kind_of_i4<kI4ZP, R, U, W, H>},
-const Variant kInt4ZpVariants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16};
+const Variant kInt4ZpVariants[] = {QV_U(1) QV_U(2) QV_U(4) QV_U(8) QV_16 QV_WB};
 #undef QV
 #undef QV_W
 #undef QV_H
 #undef QV_U
 #undef QV_16
+#undef QV_WB
 constexpr int kNumInt4 = (int)(sizeof(kInt4Variants) / sizeof(kInt4Variants[0]));
 static_assert(sizeof(kInt4Variants) == sizeof(kInt4ZpVariants), "int4 tables must match");
 

@@ -239,12 +239,18 @@ __device__ __forceinline__ bool i4_first_stands(uint32_t f_or)
 {
     return (f_or & 0x02020202u) == 0u && ((f_or & 0x01010101u) != 0u || (f_or & 0x04040404u) == 0u);
 }
-// The OR of the W flag bytes at p (4-byte aligned).
+// The OR of the W flag bytes at p (4-byte aligned), folded into the bytes of one word (the tests above look at every
+// byte).
 template <int W>
 __device__ __forceinline__ uint32_t or_flag_bytes(const uint8_t* p)
 {
-    static_assert(W == 4 || W == 8 || W == 16, "waves per block");
-    if constexpr (W == 4) {
+    static_assert(W >= 1 && W <= 16, "waves per block");
+    if constexpr (W != 4 && W != 8 && W != 16) {
+        uint32_t f = 0u;
+#pragma unroll
+        for (int w = 0; w < W; ++w) f |= (uint32_t)p[w];
+        return f;
+    } else if constexpr (W == 4) {
         return *reinterpret_cast<const uint32_t*>(p);
     } else if constexpr (W == 8) {
         const uint2 v = *reinterpret_cast<const uint2*>(p);

@@ -90,19 +90,18 @@ def test_int4_word_dot_equals_definition():
         assert abs(acc - want) <= 1e-12 * max(1.0, abs(want)), (acc, want)
 
 
-def test_fp8_upper_half_packing_exact_for_every_code():
-    """bf16 from the upper halves of the e4m3 -> f32 convert equals the e4m3fn decode for all 254 finite codes."""
-    codes = np.arange(256, dtype=np.uint8)
-    f = O.e4m3_table().astype(np.float32)[codes]       # what v_cvt_pk_f32_fp8 returns
-    bits = f.view(np.uint32)
-    # fp8x2_to_bf16x2: perm(f1, f0, 0x07060302) -> (upper half of f0, upper half of f1)
-    pairs = v_perm(bits[1::2], bits[0::2], 0x07060302)
-    lo, hi = bf16_pair(pairs)
-    dec = np.empty(256, dtype=np.float32)
-    dec[0::2], dec[1::2] = lo, hi
+def test_fp8_every_code_exact_in_bf16():
+    """The FP8 decode (v_cvt_scalef32_pk_bf16_fp8 at scale 1) writes each e4m3fn value as a bf16: exact only because
+    every finite e4m3 value has at most 4 significant bits and lies within bf16's normal range (subnormal codes
+    included), so bf16 rounding of the decoded value changes nothing; the two NaN codes stay NaN. (The instruction
+    itself is checked on the GPU over all 256 codes through every FP8 variant.)"""
+    f = O.e4m3_table().astype(np.float32)
     finite = ~np.isnan(f)
-    assert np.array_equal(dec[finite], f[finite])
-    assert np.isnan(dec[~finite]).all() and (~finite).sum() == 2        # 0x7F and 0xFF stay NaN
+    assert (~finite).sum() == 2 and np.isnan(f[[0x7F, 0xFF]]).all()
+    bf = O.bf16_bits_to_f32(O.f32_to_bf16_bits(f[finite]))
+    assert np.array_equal(bf, f[finite])
+    nz = np.abs(f[finite]) > 0
+    assert np.abs(f[finite][nz]).min() == 2.0 ** -9 and np.abs(f[finite]).max() == 448.0   # far inside bf16's range
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -172,6 +172,9 @@ KNOBS = {
 W16 = [(R, U, 16, 0) for R in (1, 2) for U in (1, 2, 4)]   # one 16-wave block per CU, row-parallel only
 for _f in ("fp8", "int4"):
     KNOBS[_f] = KNOBS[_f] + W16
+# block sizes for whole blocks per CU on the small shapes (row-parallel only)
+KNOBS["fp8"] += [(1, 2, 6, 0), (1, 2, 12, 0)]
+KNOBS["int4"] += [(1, 1, 9, 0), (2, 1, 9, 0), (1, 1, 12, 0), (1, 1, 14, 0)]
 KNOBS["int4zp"] = KNOBS["int4"]
 SHAPES = {
     "bf16": [(1, 8), (3, 264), (7, 520), (33, 1032), (129, 4104), (257, 3584), (100, 18944), (65, 4096), (17, 14336)],

@@ -44,14 +44,14 @@ def test_variant_tables_hold_harness_defaults(gemv_lib):
     """paia-bench/bench/ops/ours_bf16.py:22 and ours_quant.py:19 look these tuples up by value (KeyError otherwise)."""
     def has(vs, want):
         return any(all(v[k] == want[k] for k in "RUWSH") for v in vs)
-    assert gemv_lib.n_variants == 96 and len(gemv_lib.variants_fp8) == 42 and len(gemv_lib.variants_int4) == 54
+    assert gemv_lib.n_variants == 96 and len(gemv_lib.variants_fp8) == 44 and len(gemv_lib.variants_int4) == 58
     assert has(gemv_lib.variants, {"R": 2, "U": 4, "W": 4, "S": 0, "H": 1})
     assert has(gemv_lib.variants_fp8, {"R": 2, "U": 2, "W": 4, "S": 0, "H": 1})
     assert has(gemv_lib.variants_int4, {"R": 4, "U": 2, "W": 4, "S": 0, "H": 1})
     keys = {(v["R"], v["U"], v["W"], v["S"], v["H"]) for v in gemv_lib.variants}
     assert len(keys) == 96                                               # tuples are unique
     for kind in ("bf16", "fp8", "int4", "int4zp"):
-        n = {"bf16": 96, "fp8": 42, "int4": 54, "int4zp": 54}[kind]
+        n = {"bf16": 96, "fp8": 44, "int4": 58, "int4zp": 58}[kind]
         for N, K in [(4096, 4096), (6144, 4096), (3584, 18944), (1, 128)]:
             assert 0 <= gemv_lib.pick_variant(kind, N, K) < n
 
