@@ -92,8 +92,8 @@ __device__ __forceinline__ uint32_t f32_to_bf16_out(float f)
 // Two e4m3fn bytes (byte pair HI of word w) -> two bf16, exact for every code, in one instruction: gfx950's
 // v_cvt_scalef32_pk_bf16_fp8 (OCP e4m3) at scale 1.0. An e4m3 value has at most 4 significant bits and lies within
 // bf16's normal range, subnormal codes (m 2^-9) included, so the conversion is exact; the two NaN codes give NaN.
-// Checked on MI355X against the format's definition for all 256 codes in both byte pairs (and at scales 2^-10..2^10;
-// the instruction takes only the scale's exponent: 1.5 acts as 1.0), and by every FP8 GPU parity test. It replaces
+// Checked on MI355X against the format's definition for all 256 codes in both byte pairs (also at scales 2^-10, 0.5,
+// 2 and 2^10; the instruction takes only the scale's exponent: 1.5 acts as 1.0), and by every FP8 GPU parity test. It replaces
 // v_cvt_pk_f32_fp8 + one v_perm_b32 of the two upper halves (3 -> 2 VALU per bf16 pair with its v_dot2).
 template <bool HI>
 __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w)
