@@ -123,6 +123,27 @@ def test_every_variant_on_special_operands(oracle, gemv_lib, cuda, fmt, special,
     print(f"{special} {fmt} {n}x{K}: worst {worst:.2e} over {len(variants(gemv_lib, fmt))} variants, {sorted(kinds)}")
 
 
+# (R, W) of the INT4 variants with 9, 12 or 14 waves per block (whole blocks per CU on the small shapes)
+WHOLE_BLOCK_RW = {(1, 9), (2, 9), (1, 12), (1, 14)}
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int4zp"])
+@pytest.mark.parametrize("special", ["wide", "tiny", "huge"])
+def test_int4_whole_block_variants_on_the_subnormal_decode(oracle, gemv_lib, cuda, fmt, special):
+    """The INT4 variants with 9, 12 or 14 waves per block at a height where their waves make more than 7 weight loads,
+    so they run the subnormal decode, whose window flags are then folded over a wave count other than 4, 8 or 16: in
+    the first scale's window (wide) and outside it, where the block stages x again (tiny, huge)."""
+    n = 24576
+    o, np_ops, dev = prepared(oracle, fmt, special, cuda, N=n)
+    picked = [v for v in variants(gemv_lib, fmt) if (v["R"], v["W"]) in WHOLE_BLOCK_RW and v["H"] == 0]
+    assert len(picked) == len(WHOLE_BLOCK_RW)
+    for v in picked:
+        assert gemv_lib.launch_kind(fmt, n, K, v["id"]) == "gemv_kernel", v
+        note(f"whole-block variant {special} {fmt} {n}x{K} variant={v['id']}")
+        yb = bits16(run_gemv(gemv_lib, fmt, dev, v["id"]))
+        gate(oracle, fmt, np_ops, yb, f"{special} {fmt} {n}x{K} v{v}")
+
+
 @pytest.mark.parametrize("special", ["zeros", "large", "zeros_x100"])
 def test_int4_controls_on_special_operands(oracle, gemv_lib, cuda, special):
     """The naive (K1) control against the oracle; the unfused control against the bf16-rounded weights it uses."""
